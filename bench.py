@@ -1,0 +1,244 @@
+"""Benchmark of the paged flash-attention path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one call of the headline workload: Qwen3-4B-shaped bf16 paged decode attention
+(32 query heads, 8 KV heads, head_dim 128, 16-token pages, shuffled block tables) over a
+batch of 32 sequences of 4096 cached positions, inputs resident in HBM. Two copies of the
+KV pools alternate between steps (2 x 537 MB, over 4x the 256 MB Infinity Cache) so every
+step streams its pages from HBM. Prints ONE JSON line: decode GB/s as `value`, with the
+prefill TFLOP/s, INT8-KV decode, speculative-verify and fused RoPE + KV-write figures of
+the other BASELINE configs alongside, the roofline of the decode kernel and the CPU
+baseline (the oracle's Float32 op on the host cores, a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "tileinfer.jl_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_calls(fn, iters, warmup):
+    """Average ms per call over `iters` back-to-back calls (HIP events on the stream the
+    kernels are launched on: torch's current stream), after `warmup` calls."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        fn(i)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def decode_setup(B, L, n, Hq, Hk, D, P, copies, gen, int8=False):
+    """Pools (`copies` independent copies), block tables, q/out and workspace for B
+    sequences of L positions each with n new query tokens at positions L-n .. L-1."""
+    import torch
+    import tileinfer_hip as ti
+    per = -(-L // P)
+    pages = B * per
+    perm = torch.randperm(pages, generator=gen) + 1
+    bts = perm.view(B, per).to(torch.int32).cuda()
+    pools = []
+    for _ in range(copies):
+        if int8:
+            kq, vq = ti.int8_kv_pools(D, P, Hk, pages)
+            kq.layer_q.random_(-127, 128)
+            kq.layer_scale.uniform_(0.015, 0.03)
+            pools.append((kq, vq))
+        else:
+            k = torch.randn((pages, Hk, P, D), device="cuda", dtype=torch.bfloat16)
+            v = torch.randn((pages, Hk, P, D), device="cuda", dtype=torch.bfloat16)
+            pools.append((k, v))
+    q = torch.randn((B * n, Hq, D), device="cuda", dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    pos = (torch.arange(L - n, L, dtype=torch.int32).repeat(B)).cuda()
+    ws = ti.attention_workspace(ti.HipBackend(), q, pools[0][0], num_seqs=B, max_query_len=n)
+    return dict(pools=pools, bts=bts, q=q, out=out, pos=pos, ws=ws, n=n, B=B, L=L)
+
+
+def decode_call(s, i, scale, path=0):
+    import tileinfer_hip as ti
+    k, v = s["pools"][i % len(s["pools"])]
+    ti.paged_attention_(ti.HipBackend(), s["out"], s["ws"], s["q"], k, v, s["bts"], s["pos"],
+                        scale, True, max_query_len=s["n"], path=path)
+
+
+def decode_bytes(B, L, n, Hq, Hk, D, kv_elt_bytes):
+    """Algorithmic bytes (bench/suite.jl:248-253): read K and V once, read q, write out."""
+    return B * (2 * L * Hk * kv_elt_bytes + 2 * n * Hq * D * 2)
+
+
+def cpu_baseline(B, L, Hq, Hk, D, P, budget_s=10.0):
+    """The oracle's Float32 eager op (src/ops/reference.jl:95-121) on the host cores over
+    a sample of the headline workload, repeated for about budget_s seconds; the rate is
+    in the headline's units (bf16 algorithmic bytes of the sampled sequences per second)."""
+    import numpy as np
+    from oracle import oracle as orc
+    g = np.random.Generator(np.random.PCG64(7))
+    Bs = min(B, 4)
+    per = -(-L // P)
+    pages = Bs * per
+    kp = g.standard_normal((pages, Hk, P, D), dtype=np.float32)
+    vp = g.standard_normal((pages, Hk, P, D), dtype=np.float32)
+    bts = (g.permutation(pages) + 1).astype(np.int32).reshape(Bs, per)
+    q = g.standard_normal((Bs, Hq, D), dtype=np.float32)
+    starts = np.full(Bs, L - 1, np.int32)
+    counts = np.ones(Bs, np.int32)
+    threads = min(os.cpu_count() or 1, 16)
+    orc.attention_f32_batch(q, kp, vp, bts, starts, counts, 1 / math.sqrt(D), True, threads)
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        orc.attention_f32_batch(q, kp, vp, bts, starts, counts, 1 / math.sqrt(D), True, threads)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    gbs = decode_bytes(Bs, L, 1, Hq, Hk, D, D * 2) / dt / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{Bs} of the {B} sequences ({L} positions each, Float32 copies of the pools), "
+                      f"{reps} passes in {reps * dt:.1f} s; {dt * 1e3:.2f} ms per pass"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", default="", help="comma list: decode,prefill,int8,verify,kvwrite")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, "
+              "'How the path would shard'); run it with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import tileinfer_hip as ti
+    ti.load_library()
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    only = set(filter(None, args.only.split(",")))
+    want = lambda k: not only or k in only
+    gen = torch.Generator().manual_seed(20261201)
+    torch.manual_seed(20261201)
+    Hq, Hk, D, P = 32, 8, 128, 16
+    scale = 1 / math.sqrt(D)
+    result = {}
+
+    # ---- headline: bf16 decode, B = 32 x 4096 ----
+    B, L = 32, 4096
+    s = decode_setup(B, L, 1, Hq, Hk, D, P, 2, gen)
+    nbytes = decode_bytes(B, L, 1, Hq, Hk, D, D * 2)
+    for i in range(args.warmup):
+        decode_call(s, i, scale)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(args.steps):
+        decode_call(s, i, scale)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / args.steps
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"decode B={B} L={L}: {ms * 1e3:.1f} us/call, {gbs:.0f} GB/s ({wall:.2f} s wall)")
+    del s
+    torch.cuda.empty_cache()
+
+    extra = {}
+    if want("decode"):
+        for Bx in (1, 8):
+            sx = decode_setup(Bx, L, 1, Hq, Hk, D, P, 2, gen)
+            msx = time_calls(lambda i: decode_call(sx, i, scale), 50, 10)
+            bx = decode_bytes(Bx, L, 1, Hq, Hk, D, D * 2)
+            extra[f"decode_b{Bx}"] = {"us": round(msx * 1e3, 2), "GB/s": round(bx / msx / 1e6, 1)}
+            del sx
+    if want("verify"):
+        sv = decode_setup(16, 4096 + 16, 16, 32, 8, D, P, 2, gen)
+        msv = time_calls(lambda i: decode_call(sv, i, scale), 30, 5)
+        bv = decode_bytes(16, 4096 + 16, 16, 32, 8, D, D * 2)
+        extra["verify_qwen3_8b_b16_n16_ctx4096"] = {"us": round(msv * 1e3, 2), "GB/s": round(bv / msv / 1e6, 1),
+                                                   "pct_hbm_peak": round(100 * bv / msv / 1e6 / HBM_PEAK_GBS, 1)}
+        del sv
+    if want("int8"):
+        s8 = decode_setup(8, 32768, 1, 32, 8, D, P, 2, gen, int8=True)
+        ms8 = time_calls(lambda i: decode_call(s8, i, scale), 30, 5)
+        b8 = decode_bytes(8, 32768, 1, 32, 8, D, D + 4)
+        extra["int8_decode_llama3_8b_b8_ctx32768"] = {"us": round(ms8 * 1e3, 2), "GB/s": round(b8 / ms8 / 1e6, 1),
+                                                     "pct_hbm_peak": round(100 * b8 / ms8 / 1e6 / HBM_PEAK_GBS, 1)}
+        del s8
+    torch.cuda.empty_cache()
+    if want("prefill"):
+        for start, n in ((0, 512), (1024, 512)):
+            sp = decode_setup(1, start + n, n, Hq, Hk, D, P, 1, gen)
+            msp = time_calls(lambda i: decode_call(sp, i, scale), 50, 10)
+            visited = n * start + n * (n + 1) // 2
+            flops = 4 * D * Hq * visited
+            tf = flops / (msp * 1e-3) / 1e12
+            key = "prefill_512" if start == 0 else "chunked_prefill_512_on_1024"
+            extra[key] = {"us": round(msp * 1e3, 2), "TFLOP/s": round(tf, 1),
+                          "pct_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2), "gflop": round(flops / 1e9, 3)}
+            log(f"{key}: {msp * 1e3:.1f} us, {tf:.1f} TFLOP/s")
+            del sp
+    if want("kvwrite"):
+        n = 512
+        table = ti.RotaryTable.build(D, 4096, 1e6, torch.bfloat16)
+        qkv = torch.randn((n, (Hq + 2 * Hk) * D), device="cuda", dtype=torch.bfloat16)
+        qo = torch.empty((n, Hq, D), device="cuda", dtype=torch.bfloat16)
+        kpool = torch.zeros((64 + 32, Hk, P, D), device="cuda", dtype=torch.bfloat16)
+        vpool = torch.zeros_like(kpool)
+        positions = torch.arange(1024, 1024 + n, dtype=torch.int32, device="cuda")
+        slots_t = torch.arange(1024 + 1, 1024 + n + 1, dtype=torch.int32, device="cuda")
+        be = ti.HipBackend()
+        msk = time_calls(lambda i: ti.attention_inputs_(be, qo, kpool, vpool, qkv, None, None, table,
+                                                        positions, slots_t, 1e-6), 50, 10)
+        kb = (n * (Hq + 2 * Hk) * D * 2) + (n * Hq * D * 2) + 2 * n * Hk * D * 2 + n * 2 * D * 2
+        extra["rope_kv_write_512"] = {"us": round(msk * 1e3, 2), "GB/s": round(kb / msk / 1e6, 1)}
+
+    result = {
+        "metric": "decode attn GB/s (% of HBM peak) & prefill attn TFLOP/s at Qwen3-4B shape",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "us_per_call": round(ms * 1e3, 2),
+        "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) bf16 pools, shuffled 16-token pages)",
+        "config": {"workload": "Qwen3-4B paged decode attention (BASELINE configs[1], batch 32 x 4096 context)",
+                   "global_batch": B, "context": L, "q_heads": Hq, "kv_heads": Hk, "head_dim": D,
+                   "page_size": P, "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "note": "event time of the whole call (decode + combine kernels)"},
+    }
+    result.update(extra)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(B, L, Hq, Hk, D, P)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

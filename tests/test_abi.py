@@ -1,0 +1,124 @@
+"""The C ABI library without a GPU: it loads, exports every symbol include/*.h declares,
+and rejects bad arguments with status codes before touching the device."""
+import ctypes
+import glob
+import os
+import re
+
+import pytest
+
+import tileinfer_hip as ti
+from tileinfer_hip import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(ti_\w+)\s*\(", text))
+    return names
+
+
+def test_exports_every_declared_symbol():
+    L = ti.load_library()
+    names = declared_symbols()
+    assert names, "no declarations found"
+    assert names == set(_lib.EXPORTS)
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_version_and_status_strings():
+    L = ti.load_library()
+    assert L.ti_version().decode().startswith("tileinfer_hip")
+    assert L.ti_status_string(0) == b"ok"
+    assert L.ti_status_string(3).startswith(b"workspace")
+    assert L.ti_status_string(99) == b"unknown status"
+
+
+def _cache(**kw):
+    c = _lib.KVCache()
+    c.kind, c.head_dim, c.page_size, c.kv_heads, c.num_pages = 0, 128, 16, 8, 100
+    c.k_pages = c.v_pages = 0x1000
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+def _args(**kw):
+    a = _lib.AttentionArgs()
+    a.dtype, a.q_heads, a.num_seqs, a.max_query_len, a.total_tokens = 1, 32, 4, 1, 4
+    a.block_table_stride = 64
+    a.q = a.out = a.positions = a.block_tables = 0x1000
+    a.scale, a.causal, a.path = 0.088, 1, 0
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def ws(a, c):
+    size = ctypes.c_size_t(7)
+    st = ti.load_library().ti_attention_workspace_bytes(ctypes.byref(a), ctypes.byref(c), ctypes.byref(size))
+    return st, size.value
+
+
+def test_workspace_bytes_decode_and_prefill():
+    st, n = ws(_args(), _cache())
+    # 4 seqs x 8 KV heads -> 64 splits (2048 work-groups), 4 packed rows, (D + 2) floats
+    assert st == 0 and n == 4 * 8 * 64 * 4 * 130 * 4
+    st, n = ws(_args(max_query_len=512, total_tokens=2048), _cache())
+    assert st == 0 and n == 0                   # prefill needs none
+    st, n = ws(_args(dtype=0), _cache())
+    assert st == 0 and n == 0                   # fp32 path needs none
+    # independent of context length / pool size: same for a larger pool
+    assert ws(_args(), _cache(num_pages=100000))[1] == ws(_args(), _cache())[1]
+
+
+@pytest.mark.parametrize("bad", [
+    dict(a=dict(q_heads=30)), dict(a=dict(num_seqs=0)), dict(a=dict(q=0)),
+    dict(a=dict(total_tokens=5)), dict(a=dict(causal=2)), dict(a=dict(dtype=7)),
+    dict(a=dict(path=9)), dict(c=dict(k_pages=0)), dict(c=dict(kind=5)), dict(c=dict(page_size=0)),
+])
+def test_invalid_arguments(bad):
+    a, c = _args(**bad.get("a", {})), _cache(**bad.get("c", {}))
+    L = ti.load_library()
+    assert L.ti_attention(ctypes.byref(a), ctypes.byref(c), None) == _lib.TI_ERR_INVALID_ARG
+    assert ws(a, c)[0] == _lib.TI_ERR_INVALID_ARG
+
+
+def test_unsupported_shapes_and_workspace():
+    L = ti.load_library()
+    c = _cache(head_dim=96)
+    assert L.ti_attention(ctypes.byref(_args()), ctypes.byref(c), None) == _lib.TI_ERR_UNSUPPORTED
+    # forcing the decode kernel past its 64 packed rows
+    a = _args(max_query_len=32, total_tokens=128, path=_lib.TI_PATH_DECODE)
+    assert L.ti_attention(ctypes.byref(a), ctypes.byref(_cache()), None) == _lib.TI_ERR_UNSUPPORTED
+    # decode without (enough) workspace fails before any launch
+    assert L.ti_attention(ctypes.byref(_args()), ctypes.byref(_cache()), None) == _lib.TI_ERR_WORKSPACE
+    a = _args(workspace=0x1000, workspace_bytes=10)
+    assert L.ti_attention(ctypes.byref(a), ctypes.byref(_cache()), None) == _lib.TI_ERR_WORKSPACE
+
+
+def test_store_rope_inputs_validation():
+    L = ti.load_library()
+    c = _cache()
+    assert L.ti_store_kv(1, ctypes.byref(c), None, None, None, 0, None) == 0   # n = 0: no-op
+    assert L.ti_store_kv(1, ctypes.byref(c), None, None, None, 3, None) == _lib.TI_ERR_INVALID_ARG
+    assert L.ti_store_kv(3, ctypes.byref(c), 1, 1, 1, 3, None) == _lib.TI_ERR_INVALID_ARG
+    assert L.ti_rope(1, 1, 1, 1, 1, 10, 1, 3, 4, 127, None) == _lib.TI_ERR_INVALID_ARG   # odd D
+    assert L.ti_rope(1, None, 1, 1, 1, 10, 1, 3, 4, 128, None) == _lib.TI_ERR_INVALID_ARG
+    assert L.ti_attention_inputs(1, 1, ctypes.byref(c), 1, 1, None, 1, 10, 1, 1, 2, 16, 1e-6,
+                                 None) == _lib.TI_ERR_INVALID_ARG                        # q_norm without k_norm
+    c8 = _cache(kind=1, layer_q=0, layer_scale=0x10, smooth=0x10)
+    assert L.ti_store_kv(1, ctypes.byref(c8), 1, 1, 1, 3, None) == _lib.TI_ERR_INVALID_ARG
+
+
+def test_python_layer_rejects_host_tensors():
+    import torch
+    q = torch.zeros((1, 4, 64), dtype=torch.bfloat16)
+    with pytest.raises(ti.ArgumentError):
+        ti.attention_(ti.HipBackend(), q, None, q, torch.zeros((2, 2, 4, 64), dtype=torch.bfloat16),
+                      torch.zeros((2, 2, 4, 64), dtype=torch.bfloat16), torch.zeros(4, dtype=torch.int32),
+                      torch.zeros(1, dtype=torch.int32), 0.1)

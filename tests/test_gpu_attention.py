@@ -1,0 +1,172 @@
+"""Paged attention on the GPU (split-KV decode, MFMA prefill, fp32 path) vs the oracle.
+
+Tolerances: max abs error <= 1e-4 for fp32 and <= 2e-2 for bf16 and
+INT8-KV, against the double-accumulated oracle; also the reference's own ulp bounds
+(test/ops/tile.jl:237-259: bf16 <= 5 ulps of exact attention, INT8 <= 14 ulps of exact
+attention over the dequantized cache, whole-op relative L2 < 0.02 vs unquantized).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import tileinfer_hip as ti
+from helpers import block_table, randn, rng, smoothing, ulps
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+BE = ti.HipBackend()
+TOL = {False: 1e-4, True: 2e-2}
+
+# (head_dim, heads, kv_heads, page_size, start, n, causal): test/ops/tile.jl:217-222.
+REF_CASES = [(128, 16, 8, 64, 1023, 1, True), (128, 16, 8, 64, 63, 2, True),
+             (128, 16, 8, 64, 100, 8, True), (128, 16, 8, 64, 0, 512, True),
+             (128, 16, 8, 64, 200, 300, True), (128, 32, 8, 64, 700, 3, True),
+             (64, 12, 4, 16, 40, 5, True), (128, 32, 8, 64, 950, 16, True),
+             (128, 32, 8, 64, 63, 12, True), (128, 32, 8, 64, 1000, 16, False),
+             (128, 32, 8, 64, 300, 30, False)]
+# Shapes the BASELINE configs add: 16-token pages, tiny pages, page-straddling steps.
+EXTRA_CASES = [(128, 32, 8, 16, 1500, 1, True), (128, 32, 8, 16, 4000, 16, True),
+               (128, 32, 8, 4, 37, 9, True), (128, 8, 8, 16, 77, 3, True),
+               (128, 64, 8, 16, 120, 8, True), (64, 8, 2, 32, 0, 1, True),
+               (128, 32, 8, 16, 1024, 512, True), (128, 16, 8, 16, 0, 100, False)]
+
+
+def dev(x, dtype):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(dtype).cuda()
+
+
+def make_case(case, bf16, seed):
+    D, H, KVH, P, start, n, causal = case
+    g = rng(seed)
+    L = start + n
+    pages = -(-L // P) + 2
+    bt = block_table(g, L, P, pages)
+    q = randn(g, n, H, D, bf16=bf16)
+    kp, vp = randn(g, pages, KVH, P, D, bf16=bf16), randn(g, pages, KVH, P, D, bf16=bf16)
+    return dict(q=q, kp=kp, vp=vp, bt=bt, start=start, n=n, causal=causal, D=D, g=g)
+
+
+def run_gpu(c, dtype, path=ti.TI_PATH_AUTO, k=None, v=None):
+    q = dev(c["q"], dtype)
+    k = dev(c["kp"], dtype) if k is None else k
+    v = dev(c["vp"], dtype) if v is None else v
+    out = torch.empty_like(q)
+    ws = ti.attention_workspace(BE, q, k, path=path)
+    pos = torch.arange(c["start"], c["start"] + c["n"], dtype=torch.int32, device="cuda")
+    ti.attention_(BE, out, ws, q, k, v, torch.from_numpy(c["bt"]).cuda(), pos,
+                  1 / math.sqrt(c["D"]), c["causal"], path=path)
+    return out.float().cpu().numpy()
+
+
+def exact(c, **kw):
+    if "layer_q" in kw:
+        return orc.attention(c["q"], c["bt"], c["start"], 1 / math.sqrt(c["D"]), c["causal"], **kw)
+    return orc.attention(c["q"], c["bt"], c["start"], 1 / math.sqrt(c["D"]), c["causal"],
+                         kw.get("kp", c["kp"]), kw.get("vp", c["vp"]))
+
+
+def check(ref, got, bf16):
+    err = float(np.max(np.abs(ref - got)))
+    assert err <= TOL[bf16], f"max abs err {err}"
+    if bf16:
+        u = ulps(ref, got)
+        assert u <= 5, f"{u} ulps"
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("case", REF_CASES + EXTRA_CASES, ids=str)
+def test_attention(gpu, case, bf16):
+    c = make_case(case, bf16, seed=hash(case) % 10000 + bf16)
+    dtype = torch.bfloat16 if bf16 else torch.float32
+    ref = exact(c)
+    check(ref, run_gpu(c, dtype), bf16)
+    if bf16:
+        D, H, KVH, P, start, n, causal = case
+        # both MFMA kernels wherever their shape limits allow
+        if (H // KVH) * n <= 64:
+            check(ref, run_gpu(c, dtype, ti.TI_PATH_DECODE), True)
+        if n <= 16:
+            check(ref, run_gpu(c, dtype, ti.TI_PATH_PREFILL), True)
+
+
+@pytest.mark.parametrize("case", REF_CASES + EXTRA_CASES[:5], ids=str)
+def test_attention_int8(gpu, case):
+    """INT8 cache (bf16 activations), keys scaled like the smoothing factors."""
+    D, H, KVH, P, start, n, causal = case
+    c = make_case(case, True, seed=hash(case) % 10000 + 7)
+    g = c["g"]
+    cs = smoothing(g, D)
+    pages = c["kp"].shape[0]
+    k_src = orc.bf16_round(c["kp"] * orc.bf16_round(cs)[None, None, None, :])
+    kq, vq = ti.int8_kv_pools(D, P, KVH, pages, key_smoothing=torch.from_numpy(cs))
+    # every position of the pool, through the GPU store (bit-exact vs the oracle's)
+    kk = dev(k_src.transpose(0, 2, 1, 3).reshape(-1, KVH, D), torch.bfloat16)
+    vv = dev(c["vp"].transpose(0, 2, 1, 3).reshape(-1, KVH, D), torch.bfloat16)
+    ti.store_kv_(BE, kq, vq, kk, vv, torch.arange(1, P * pages + 1, dtype=torch.int32, device="cuda"))
+    lq, ls = kq.layer_q.cpu().numpy(), kq.layer_scale.cpu().numpy()
+    ref8 = exact(c, layer_q=lq, layer_scale=ls, smooth=cs)
+    paths = [ti.TI_PATH_AUTO]
+    if (H // KVH) * n <= 64 and n > 16:
+        paths.append(ti.TI_PATH_DECODE)
+    if n <= 16:
+        paths.append(ti.TI_PATH_PREFILL)
+    for path in paths:
+        y8 = run_gpu(c, torch.bfloat16, path, kq, vq)
+        assert float(np.max(np.abs(ref8 - y8))) <= 2e-2
+        assert ulps(ref8, y8) <= 14
+        src = exact(c, kp=k_src, vp=c["vp"])
+        rel = math.sqrt(float(np.sum((y8 - src) ** 2)) / float(np.sum(src ** 2)))
+        assert rel < 0.02
+
+
+@pytest.mark.parametrize("path", [ti.TI_PATH_AUTO, ti.TI_PATH_PREFILL])
+def test_batched_ragged(gpu, path):
+    """B sequences of different lengths and query counts (one empty) in one call."""
+    g = rng(900 + path)
+    D, H, KVH, P = 128, 32, 8, 16
+    starts = [700, 0, 33, 2000, 5]
+    counts = [3, 16, 0, 1, 9] if path == ti.TI_PATH_AUTO else [40, 130, 0, 1, 64]
+    nmax = max(counts)
+    pages = sum(-(-(s + n) // P) for s, n in zip(starts, counts)) + 3
+    perm = g.permutation(pages) + 1
+    width = 160
+    bts = np.zeros((len(starts), width), np.int32)
+    off = 0
+    for b, (s, n) in enumerate(zip(starts, counts)):
+        used = -(-(s + n) // P)
+        bts[b, :used] = perm[off:off + used]
+        off += used
+    kp, vp = randn(g, pages, KVH, P, D, bf16=True), randn(g, pages, KVH, P, D, bf16=True)
+    T = sum(counts)
+    q = randn(g, T, H, D, bf16=True)
+    qsl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    positions = np.concatenate([np.arange(s, s + n) for s, n in zip(starts, counts)]).astype(np.int32)
+    qd = dev(q, torch.bfloat16)
+    out = torch.zeros_like(qd)
+    kd, vd = dev(kp, torch.bfloat16), dev(vp, torch.bfloat16)
+    ws = ti.attention_workspace(BE, qd, kd, num_seqs=len(starts), max_query_len=nmax, path=path)
+    ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(),
+                        torch.from_numpy(positions).cuda(), 1 / math.sqrt(D), True,
+                        query_start_loc=torch.from_numpy(qsl).cuda(), max_query_len=nmax, path=path)
+    got = out.float().cpu().numpy()
+    for b, (s, n) in enumerate(zip(starts, counts)):
+        if n == 0:
+            continue
+        ref = orc.attention(q[qsl[b]:qsl[b + 1]], bts[b], s, 1 / math.sqrt(D), True, kp, vp)
+        check(ref, got[qsl[b]:qsl[b + 1]], True)
+
+
+def test_workspace_errors(gpu):
+    c = make_case((128, 16, 8, 16, 100, 1, True), True, 1)
+    q = dev(c["q"], torch.bfloat16)
+    k = dev(c["kp"], torch.bfloat16)
+    out = torch.empty_like(q)
+    pos = torch.tensor([100], dtype=torch.int32, device="cuda")
+    bt = torch.from_numpy(c["bt"]).cuda()
+    with pytest.raises(ti.WorkspaceError):
+        ti.attention_(BE, out, None, q, k, k, bt, pos, 0.1)
+    small = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(ti.WorkspaceError):
+        ti.attention_(BE, out, small, q, k, k, bt, pos, 0.1)

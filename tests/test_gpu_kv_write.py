@@ -1,0 +1,152 @@
+"""RoPE, KV-cache writes and the fused attention-input op on the GPU vs the CPU oracle.
+
+All bit-exact (test/ops/tile.jl:41-47, :63-89, :111-146), except the q/k RMSNorm path,
+whose sum of squares runs in a different order (<= 1 bf16 ulp, as the reference's own
+tolerance for it, test/ops/tile.jl:133-134).
+"""
+import numpy as np
+import pytest
+import torch
+
+import tileinfer_hip as ti
+from helpers import randn, rng, smoothing, ulps
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+BE = ti.HipBackend()
+DT = {False: torch.float32, True: torch.bfloat16}
+
+
+def dev(x, bf16=False):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(DT[bf16]).cuda()
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("dims", [(128, 16, 1), (128, 8, 7), (64, 24, 3)])
+def test_rope_bit_exact(gpu, bf16, dims):
+    D, H, n = dims
+    g = rng(100 + D + H + n)
+    x = randn(g, n, H, D, bf16=bf16)
+    theta = g.random((50, D // 2), dtype=np.float32) * 100
+    c, s = np.cos(np.concatenate([theta, theta], 1)), np.sin(np.concatenate([theta, theta], 1))
+    c, s = (orc.bf16_round(c), orc.bf16_round(s)) if bf16 else (c.astype(np.float32), s.astype(np.float32))
+    pos = g.integers(0, 50, n).astype(np.int32)
+    y = ti.rope(BE, dev(x, bf16), dev(c, bf16), dev(s, bf16), torch.from_numpy(pos).cuda())
+    assert np.array_equal(host(y), orc.rope(x, c, s, pos, bf16))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_store_kv_bit_exact(gpu, bf16):
+    D, P, H, pages, n = 128, 4, 8, 6, 9
+    g = rng(200 + bf16)
+    k, v = randn(g, n, H, D, bf16=bf16), randn(g, n, H, D, bf16=bf16)
+    slots = np.array([13, 14, 15, 16, 5, 6, 7, 8, 21], np.int32)
+    kp = torch.zeros((pages, H, P, D), dtype=DT[bf16], device="cuda")
+    vp = torch.zeros_like(kp)
+    ti.store_kv_(BE, kp, vp, dev(k, bf16), dev(v, bf16), torch.from_numpy(slots).cuda())
+    rk, rv = np.zeros((pages, H, P, D), np.float32), np.zeros((pages, H, P, D), np.float32)
+    orc.store_kv(rk, rv, k, v, slots)
+    assert np.array_equal(host(kp), rk) and np.array_equal(host(vp), rv)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("smooth", [False, True])
+def test_store_kv_int8_bit_exact(gpu, bf16, smooth):
+    D, P, H, pages, n = 128, 4, 8, 6, 9
+    g = rng(300 + 2 * bf16 + smooth)
+    k, v = randn(g, n, H, D, bf16=bf16), randn(g, n, H, D, bf16=bf16)
+    slots = np.array([13, 14, 15, 16, 5, 6, 7, 8, 21], np.int32)
+    c = smoothing(g, D) if smooth else np.ones(D, np.float32)
+    kq, vq = ti.int8_kv_pools(D, P, H, pages, key_smoothing=torch.from_numpy(c) if smooth else None)
+    ti.store_kv_(BE, kq, vq, dev(k, bf16), dev(v, bf16), torch.from_numpy(slots).cuda())
+    lq = np.zeros((2, pages, H, P, D), np.int8)
+    ls = np.zeros((2, pages, H, P), np.float32)
+    orc.store_kv_int8(lq, ls, c, k, v, slots)
+    assert np.array_equal(kq.layer_q.cpu().numpy(), lq)
+    assert np.array_equal(kq.layer_scale.cpu().numpy(), ls)
+    # known answers (test/ops/tile.jl:76-81) on slot 13 = offset 0 of page 4
+    x = k[0, 0] / c
+    s = ls[0, 3, 0, 0]
+    assert s == pytest.approx(np.abs(x).max() / 127, rel=1e-6)
+    assert np.abs(lq[0, 3, 0, 0].astype(np.int32)).max() == 127
+
+
+def _table(g, D, L, bf16):
+    theta = g.random((L, D // 2), dtype=np.float32) * 100
+    ang = np.concatenate([theta, theta], 1)
+    c, s = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    if bf16:
+        c, s = orc.bf16_round(c), orc.bf16_round(s)
+    return c, s, ti.RotaryTable.from_arrays(torch.from_numpy(c), torch.from_numpy(s), DT[bf16])
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_attention_inputs(gpu, bf16, qk_norm):
+    # test/ops/tile.jl:111-146: positions [3,17,18,40,0], slots [13,14,15,16,70].
+    D, nq, nkv, P, pages, L = 128, 16, 8, 16, 6, 64
+    g = rng(400 + 2 * bf16 + qk_norm)
+    positions = np.array([3, 17, 18, 40, 0], np.int32)
+    slots = np.array([13, 14, 15, 16, 70], np.int32)
+    n = len(positions)
+    c, s, table = _table(g, D, L, bf16)
+    qkv = randn(g, n, nq + 2 * nkv, D, bf16=bf16)
+    qn, kn = (randn(g, D, bf16=bf16), randn(g, D, bf16=bf16)) if qk_norm else (None, None)
+    pos_d, slots_d = torch.from_numpy(positions).cuda(), torch.from_numpy(slots).cuda()
+
+    q = torch.zeros((n, nq, D), dtype=DT[bf16], device="cuda")
+    kp = torch.zeros((pages, nkv, P, D), dtype=DT[bf16], device="cuda")
+    vp = torch.zeros_like(kp)
+    ti.attention_inputs_(BE, q, kp, vp, dev(qkv, bf16), None if qn is None else dev(qn, bf16),
+                         None if kn is None else dev(kn, bf16), table, pos_d, slots_d, 1e-6)
+    rkp, rvp = np.zeros((pages, nkv, P, D), np.float32), np.zeros((pages, nkv, P, D), np.float32)
+    rq = orc.attention_inputs(qkv, qn, kn, np.stack([c, s], 1), positions, slots, nq, nkv, 1e-6, bf16,
+                              k_pages=rkp, v_pages=rvp)
+    if not qk_norm:
+        assert np.array_equal(host(q), rq)
+        assert np.array_equal(host(kp), rkp) and np.array_equal(host(vp), rvp)
+        # fused == the primitive ops chained (rope_ then store_kv_), bit-identical
+        kp2, vp2 = torch.zeros_like(kp), torch.zeros_like(kp)
+        qkv_d = dev(qkv, bf16)
+        qs = qkv_d[:, :nq].contiguous()
+        kk = qkv_d[:, nq:nq + nkv].contiguous()
+        vv = qkv_d[:, nq + nkv:].contiguous()
+        q2 = ti.rope(BE, qs, table.cos, table.sin, pos_d)
+        ti.store_kv_(BE, kp2, vp2, ti.rope(BE, kk, table.cos, table.sin, pos_d), vv, slots_d)
+        assert torch.equal(q2, q) and torch.equal(kp2, kp) and torch.equal(vp2, vp)
+    else:
+        worst = max(ulps(r, host(f)) for r, f in ((rq, q), (rkp, kp), (rvp, vp)))
+        assert worst <= (1 if bf16 else 32)
+
+    # into an INT8 cache: quantized as store_kv! quantizes (known when no norm: bit-exact)
+    cs = smoothing(g, D)
+    kq, vq = ti.int8_kv_pools(D, P, nkv, pages, key_smoothing=torch.from_numpy(cs))
+    q8 = torch.zeros_like(q)
+    ti.attention_inputs_(BE, q8, kq, vq, dev(qkv, bf16), None if qn is None else dev(qn, bf16),
+                         None if kn is None else dev(kn, bf16), table, pos_d, slots_d, 1e-6)
+    lq = np.zeros((2, pages, nkv, P, D), np.int8)
+    ls = np.zeros((2, pages, nkv, P), np.float32)
+    orc.attention_inputs(qkv, qn, kn, np.stack([c, s], 1), positions, slots, nq, nkv, 1e-6, bf16,
+                         layer_q=lq, layer_scale=ls, smooth=cs)
+    assert torch.equal(q8, q)
+    if not qk_norm:
+        assert np.array_equal(kq.layer_q.cpu().numpy(), lq)
+        assert np.array_equal(kq.layer_scale.cpu().numpy(), ls)
+    else:
+        assert np.abs(kq.layer_q.cpu().numpy().astype(np.int32) - lq).max() <= 1
+        assert np.allclose(kq.layer_scale.cpu().numpy(), ls, rtol=1e-2)
+
+
+def test_out_of_range_slots_are_skipped(gpu):
+    D, P, H, pages = 64, 4, 2, 3
+    k = torch.ones((3, H, D), dtype=torch.bfloat16, device="cuda")
+    kp = torch.zeros((pages, H, P, D), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    ti.store_kv_(BE, kp, vp, k, k, torch.tensor([0, 13, 2], dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    assert kp.sum().item() == H * D                     # only slot 2 was written
+    assert kp[0, :, 1].float().eq(1).all()

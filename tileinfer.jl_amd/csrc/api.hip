@@ -1,0 +1,126 @@
+// C ABI of libtileinfer_hip: argument validation (host only, before any HIP call) and
+// dispatch to the kernels. See include/tileinfer_hip.h for the contract of each entry.
+#include "common.hpp"
+
+namespace {
+
+bool bad_cache(const ti_kv_cache *c, bool need_attention_dims) {
+    if (!c) return true;
+    if (c->kind != TI_KV_DENSE && c->kind != TI_KV_INT8) return true;
+    if (c->head_dim <= 0 || (c->head_dim & 1) || c->page_size <= 0 || c->kv_heads <= 0 ||
+        c->num_pages <= 0)
+        return true;
+    if (c->kind == TI_KV_DENSE && (!c->k_pages || !c->v_pages)) return true;
+    if (c->kind == TI_KV_INT8 && (!c->layer_q || !c->layer_scale || !c->smooth)) return true;
+    (void)need_attention_dims;
+    return false;
+}
+
+bool bad_dtype(int dtype) { return dtype != TI_F32 && dtype != TI_BF16; }
+
+// Resolve the kernel family of an attention call: 0 generic (fp32), 1 decode, 2 prefill,
+// or a negative ti_status.
+int resolve_path(const ti_attention_args *a, const ti_kv_cache *c) {
+    const int G = a->q_heads / c->kv_heads;
+    if (a->dtype == TI_F32) return 0;
+    const bool decode_ok = G * a->max_query_len <= 64;
+    switch (a->path) {
+        case TI_PATH_AUTO: return (a->max_query_len <= 16 && decode_ok) ? 1 : (G <= 64 ? 2 : -TI_ERR_UNSUPPORTED);
+        case TI_PATH_DECODE: return decode_ok ? 1 : -TI_ERR_UNSUPPORTED;
+        case TI_PATH_PREFILL: return G <= 64 ? 2 : -TI_ERR_UNSUPPORTED;
+        default: return -TI_ERR_INVALID_ARG;
+    }
+}
+
+int check_attention(const ti_attention_args *a, const ti_kv_cache *c) {
+    if (!a || bad_cache(c, true) || bad_dtype(a->dtype)) return TI_ERR_INVALID_ARG;
+    if (c->head_dim != 64 && c->head_dim != 128) return TI_ERR_UNSUPPORTED;
+    if (a->q_heads <= 0 || a->q_heads % c->kv_heads) return TI_ERR_INVALID_ARG;
+    if (a->num_seqs <= 0 || a->max_query_len <= 0 || a->total_tokens <= 0 ||
+        a->block_table_stride <= 0)
+        return TI_ERR_INVALID_ARG;
+    if (!a->q || !a->out || !a->positions || !a->block_tables) return TI_ERR_INVALID_ARG;
+    if (!a->query_start_loc && (long long)a->num_seqs * a->max_query_len != a->total_tokens)
+        return TI_ERR_INVALID_ARG;
+    if (a->causal != 0 && a->causal != 1) return TI_ERR_INVALID_ARG;
+    if (!(a->scale == a->scale)) return TI_ERR_INVALID_ARG;
+    return TI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *ti_version(void) { return "tileinfer_hip 0.1.0 gfx950"; }
+
+const char *ti_status_string(int status) {
+    switch (status) {
+        case TI_OK: return "ok";
+        case TI_ERR_INVALID_ARG: return "invalid argument";
+        case TI_ERR_UNSUPPORTED: return "unsupported shape or type";
+        case TI_ERR_WORKSPACE: return "workspace missing or too small";
+        case TI_ERR_LAUNCH: return "kernel launch failed";
+        default: return "unknown status";
+    }
+}
+
+int ti_attention_workspace_bytes(const ti_attention_args *a, const ti_kv_cache *c, size_t *bytes) {
+    if (!bytes) return TI_ERR_INVALID_ARG;
+    *bytes = 0;
+    int st = check_attention(a, c);
+    if (st) return st;
+    const int path = resolve_path(a, c);
+    if (path < 0) return -path;
+    if (path == 1) *bytes = ti_plan_decode(a, c).bytes;
+    return TI_OK;
+}
+
+int ti_attention(const ti_attention_args *a, const ti_kv_cache *c, void *stream) {
+    int st = check_attention(a, c);
+    if (st) return st;
+    const int path = resolve_path(a, c);
+    if (path < 0) return -path;
+    hipStream_t s = (hipStream_t)stream;
+    if (path == 0) return ti_launch_generic(a, c, s);
+    if (path == 2) return ti_launch_prefill(a, c, s);
+    const ti_decode_plan pl = ti_plan_decode(a, c);
+    if (!a->workspace || a->workspace_bytes < pl.bytes) return TI_ERR_WORKSPACE;
+    return ti_launch_decode(a, c, pl, s);
+}
+
+int ti_store_kv(int dtype, const ti_kv_cache *c, const void *k, const void *v,
+                const int32_t *slots, int n, void *stream) {
+    if (bad_dtype(dtype) || bad_cache(c, false) || n < 0) return TI_ERR_INVALID_ARG;
+    if (c->head_dim > 512) return TI_ERR_UNSUPPORTED;
+    if (n == 0) return TI_OK;
+    if (!k || !v || !slots) return TI_ERR_INVALID_ARG;
+    return ti_launch_store_kv(dtype, c, k, v, slots, n, (hipStream_t)stream);
+}
+
+int ti_rope(int dtype, void *y, const void *x, const void *cos_table, const void *sin_table,
+            int table_len, const int32_t *positions, int n, int heads, int head_dim,
+            void *stream) {
+    if (bad_dtype(dtype) || n < 0 || heads <= 0 || head_dim <= 0 || (head_dim & 1) ||
+        table_len <= 0)
+        return TI_ERR_INVALID_ARG;
+    if (n == 0) return TI_OK;
+    if (!y || !x || !cos_table || !sin_table || !positions) return TI_ERR_INVALID_ARG;
+    return ti_launch_rope(dtype, y, x, cos_table, sin_table, table_len, positions, n, heads,
+                          head_dim, (hipStream_t)stream);
+}
+
+int ti_attention_inputs(int dtype, void *q_out, const ti_kv_cache *c, const void *qkv,
+                        const void *q_norm, const void *k_norm, const void *cos_sin,
+                        int table_len, const int32_t *positions, const int32_t *slots, int n,
+                        int q_heads, float eps, void *stream) {
+    if (bad_dtype(dtype) || bad_cache(c, false) || n < 0 || q_heads <= 0 || table_len <= 0)
+        return TI_ERR_INVALID_ARG;
+    if (c->head_dim > 128) return TI_ERR_UNSUPPORTED;
+    if ((q_norm == nullptr) != (k_norm == nullptr)) return TI_ERR_INVALID_ARG;
+    if (n == 0) return TI_OK;
+    if (!q_out || !qkv || !cos_sin || !positions || !slots) return TI_ERR_INVALID_ARG;
+    return ti_launch_attention_inputs(dtype, q_out, c, qkv, q_norm, k_norm, cos_sin, table_len,
+                                      positions, slots, n, q_heads, eps, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,103 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of libtileinfer_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tileinfer_hip.h"
+
+namespace ti {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVE = 64;
+// Finite stand-in for -inf as the initial running max: a row whose keys are all masked
+// keeps m = NEG_BIG, l = 0 and gets weight 0 when splits are combined (no inf - inf).
+constexpr float NEG_BIG = -3.402823466e38f;
+constexpr float LOG2E = 1.4426950408889634f;
+
+// bf16 storage is uint16_t; arithmetic is in float.
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// Round to nearest even (gfx950's v_cvt_pk_bf16_f32 through the __bf16 conversion).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    __bf16 h = (__bf16)f;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+// Element type traits: load as float, round a float to T (kept as float), store.
+template <typename T> struct Elt;
+template <> struct Elt<float> {
+    static __device__ __forceinline__ float ld(const float *p, size_t i) { return p[i]; }
+    static __device__ __forceinline__ float rnd(float x) { return x; }
+    static __device__ __forceinline__ void st(float *p, size_t i, float x) { p[i] = x; }
+};
+template <> struct Elt<uint16_t> {
+    static __device__ __forceinline__ float ld(const uint16_t *p, size_t i) { return bf2f(p[i]); }
+    static __device__ __forceinline__ float rnd(float x) { return bf2f(f2bf(x)); }
+    static __device__ __forceinline__ void st(uint16_t *p, size_t i, float x) { p[i] = f2bf(x); }
+};
+
+// Two floats -> one word of two bf16 (round to nearest even), low element first.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// MFMA operands are assembled from 32-bit words and bit-cast whole; building bf16
+// vectors element by element has been seen to miscompile (only element 0 kept).
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
+
+// 4 int8 (one word) -> 2 words of bf16 (exact).
+__device__ __forceinline__ void i8x4_to_bf16(uint32_t v, uint32_t &lo, uint32_t &hi) {
+    lo = pack_bf16x2((float)(int8_t)(v), (float)(int8_t)(v >> 8));
+    hi = pack_bf16x2((float)(int8_t)(v >> 16), (float)(int8_t)(v >> 24));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Block-table lookup with the 1-based page id clamped into the pool, so a malformed
+// table can never send a load outside the pool.
+__device__ __forceinline__ int page_of(const int32_t *bt, int idx, int num_pages) {
+    int p = bt[idx] - 1;
+    p = p < 0 ? 0 : p;
+    return p >= num_pages ? num_pages - 1 : p;
+}
+
+}  // namespace ti
+
+// Launchers implemented per kernel file, dispatched by api.hip.
+int ti_launch_rope(int dtype, void *y, const void *x, const void *cos_t, const void *sin_t,
+                   int table_len, const int32_t *positions, int n, int heads, int D,
+                   hipStream_t s);
+int ti_launch_store_kv(int dtype, const ti_kv_cache *c, const void *k, const void *v,
+                       const int32_t *slots, int n, hipStream_t s);
+int ti_launch_attention_inputs(int dtype, void *q_out, const ti_kv_cache *c, const void *qkv,
+                               const void *q_norm, const void *k_norm, const void *cos_sin,
+                               int table_len, const int32_t *positions, const int32_t *slots,
+                               int n, int q_heads, float eps, hipStream_t s);
+
+struct ti_decode_plan {
+    int splits;      // split-KV work-groups per (sequence, KV head)
+    int rows;        // packed query rows G * max_query_len
+    size_t bytes;    // workspace bytes
+};
+ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c);
+int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_decode_plan &p,
+                     hipStream_t s);
+int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s);
+int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s);

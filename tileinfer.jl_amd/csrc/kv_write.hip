@@ -1,0 +1,287 @@
+// KV-cache writes, rotary embedding and the fused attention-input op.
+//
+// All three are HBM-bound element-wise kernels whose results must be bit-identical to the
+// reference's: every product and sum is rounded separately, so contraction into FMA is
+// disabled for the whole file.
+#pragma clang fp contract(off)
+
+#include "common.hpp"
+
+using namespace ti;
+
+namespace {
+
+// Pool row (0-based, in units of D elements) of (1-based slot, KV head h) in a
+// [pages][H][P][D] pool: offset + P h + P H page (src/ops/reference.jl:61-70,
+// src/ops/tile/elementwise.jl:122-128). Returns -1 for a slot outside the pool.
+__device__ __forceinline__ long long slot_row(int32_t slot, int h, int P, int H, int pages) {
+    long long s = (long long)slot - 1;
+    if (s < 0 || s >= (long long)P * pages) return -1;
+    return (s % P) + (long long)P * h + (long long)P * H * (s / P);
+}
+
+// ---- rope (src/ops/tile/elementwise.jl:10-27; reference src/ops/reference.jl:32-39) ----
+// y1 = rnd(rnd(x1 c1) + rnd(-x2 s1)), y2 = rnd(rnd(x2 c2) + rnd(x1 s2)), rnd = round to T.
+template <typename T>
+__global__ void __launch_bounds__(256) rope_kernel(T *__restrict__ y, const T *__restrict__ x,
+                                                   const T *__restrict__ cos_t,
+                                                   const T *__restrict__ sin_t, int table_len,
+                                                   const int32_t *__restrict__ positions,
+                                                   int heads, int D) {
+    using E = Elt<T>;
+    const int t = blockIdx.y, half = D / 2;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= heads * half) return;
+    const int p = positions[t];
+    if (p < 0 || p >= table_len) return;
+    const int h = idx / half, i = idx % half;
+    const size_t base = ((size_t)t * heads + h) * D, tab = (size_t)p * D;
+    const float a = E::ld(x, base + i), b = E::ld(x, base + i + half);
+    const float c1 = E::ld(cos_t, tab + i), c2 = E::ld(cos_t, tab + i + half);
+    const float s1 = E::ld(sin_t, tab + i), s2 = E::ld(sin_t, tab + i + half);
+    E::st(y, base + i, E::rnd(E::rnd(a * c1) + E::rnd(-b * s1)));
+    E::st(y, base + i + half, E::rnd(E::rnd(b * c2) + E::rnd(a * s2)));
+}
+
+// ---- dense store_kv (src/ops/tile/elementwise.jl:119-131): bit copies, 16 B per lane ----
+// Grid (n, H), one wave per (token, head): K and V rows of D elements.
+template <typename T>
+__global__ void __launch_bounds__(64) store_kv_kernel(T *__restrict__ kp, T *__restrict__ vp,
+                                                      const T *__restrict__ k,
+                                                      const T *__restrict__ v,
+                                                      const int32_t *__restrict__ slots, int D,
+                                                      int P, int H, int pages) {
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const long long row = slot_row(slots[t], h, P, H, pages);
+    if (row < 0) return;
+    const size_t src = ((size_t)t * H + h) * D, dst = (size_t)row * D;
+    const int bytes = D * (int)sizeof(T);
+    if ((bytes & 15) == 0) {
+        const uint4 *ks = reinterpret_cast<const uint4 *>(k + src);
+        const uint4 *vs = reinterpret_cast<const uint4 *>(v + src);
+        uint4 *kd = reinterpret_cast<uint4 *>(kp + dst);
+        uint4 *vd = reinterpret_cast<uint4 *>(vp + dst);
+        for (int i = lane; i < bytes / 16; i += WAVE) {
+            kd[i] = ks[i];
+            vd[i] = vs[i];
+        }
+    } else {
+        for (int i = lane; i < D; i += WAVE) {
+            kp[dst + i] = k[src + i];
+            vp[dst + i] = v[src + i];
+        }
+    }
+}
+
+// Quantize one vector held as up to 8 values per lane (element i = lane + 64 j) into q at
+// row `row` and its scale, as quantize_columns (src/ops/quant.jl:141-145) and store_int8!
+// (src/ops/tile/elementwise.jl:154-161): absmax = max|x|; inv = absmax > 0 ? 127/absmax : 0;
+// q = Int8(floor(x inv + 1/2)); s = absmax / 127. All lanes of the wave must call it.
+__device__ __forceinline__ void quantize_store(const float (&x)[8], int D, int8_t *__restrict__ q,
+                                               float *__restrict__ scale, size_t row) {
+    const int lane = threadIdx.x;
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+        if (lane + WAVE * j < D) m = fmaxf(m, fabsf(x[j]));
+    const float absmax = wave_max(m);
+    const float inv = absmax > 0.0f ? __fdiv_rn(127.0f, absmax) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = lane + WAVE * j;
+        if (i < D) q[row * D + i] = (int8_t)floorf(__fadd_rn(__fmul_rn(x[j], inv), 0.5f));
+    }
+    if (lane == 0) scale[row] = __fdiv_rn(absmax, 127.0f);
+}
+
+// ---- INT8 store_kv (src/ops/tile/elementwise.jl:163-178; src/ops/quant.jl:147-159) ----
+// Keys are divided by the smoothing factors first; values are not.
+template <typename T>
+__global__ void __launch_bounds__(64) store_kv_int8_kernel(int8_t *__restrict__ lq,
+                                                           float *__restrict__ ls,
+                                                           const float *__restrict__ smooth,
+                                                           const T *__restrict__ k,
+                                                           const T *__restrict__ v,
+                                                           const int32_t *__restrict__ slots,
+                                                           int D, int P, int H, int pages) {
+    using E = Elt<T>;
+    const int t = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const long long row = slot_row(slots[t], h, P, H, pages);
+    if (row < 0) return;  // uniform across the wave
+    const size_t src = ((size_t)t * H + h) * D;
+    const size_t half_q = (size_t)pages * H * P * D, half_s = (size_t)pages * H * P;
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = lane + WAVE * j;
+        x[j] = i < D ? __fdiv_rn(E::ld(k, src + i), smooth[i]) : 0.0f;
+    }
+    quantize_store(x, D, lq, ls, (size_t)row);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int i = lane + WAVE * j;
+        x[j] = i < D ? E::ld(v, src + i) : 0.0f;
+    }
+    quantize_store(x, D, lq + half_q, ls + half_s, (size_t)row);
+}
+
+// ---- fused attention inputs (src/ops/tile/fused.jl:15-92) ----
+// Grid (n, nq + nkv), one wave per (token, head). Lane i < D/2 owns the rotary pair
+// (i, i + D/2). Heads j < nq are queries -> q_out; the others are KV head h = j - nq:
+// the key (normed, rotated) and the value go to the cache at slots[t].
+template <typename T, bool NORM, bool INT8>
+__global__ void __launch_bounds__(64) attention_inputs_kernel(
+    T *__restrict__ q_out, T *__restrict__ kp, T *__restrict__ vp, int8_t *__restrict__ lq,
+    float *__restrict__ ls, const float *__restrict__ smooth, const T *__restrict__ qkv,
+    const T *__restrict__ q_norm, const T *__restrict__ k_norm, const T *__restrict__ cos_sin,
+    int table_len, const int32_t *__restrict__ positions, const int32_t *__restrict__ slots,
+    int nq, int nkv, int D, int P, int pages, float eps) {
+    using E = Elt<T>;
+    const int t = blockIdx.x, j = blockIdx.y, lane = threadIdx.x, half = D / 2;
+    const bool is_q = j < nq;
+    const int h = j - nq;
+    const int pos = positions[t];
+    if (pos < 0 || pos >= table_len) return;
+    long long row = 0;
+    if (!is_q) {
+        row = slot_row(slots[t], h, P, nkv, pages);
+        if (row < 0) return;
+    }
+    const size_t col = ((size_t)t * (nq + 2 * nkv) + j) * D;
+    const bool on = lane < half;
+    float a = on ? E::ld(qkv, col + lane) : 0.0f;
+    float b = on ? E::ld(qkv, col + lane + half) : 0.0f;
+    if (NORM) {
+        // rmsnorm in Float32, rounding as rmsnorm_kernel: rnd(rnd(x inv_rms) w).
+        const float ss = wave_sum(a * a + b * b);
+        const float inv_rms = __frcp_rn(__fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+        const T *w = is_q ? q_norm : k_norm;
+        if (on) {
+            a = E::rnd(E::rnd(a * inv_rms) * E::ld(w, lane));
+            b = E::rnd(E::rnd(b * inv_rms) * E::ld(w, lane + half));
+        }
+    }
+    const size_t cs = (size_t)pos * 2 * D;
+    float y1 = 0.0f, y2 = 0.0f;
+    if (on) {
+        const float c1 = E::ld(cos_sin, cs + lane), c2 = E::ld(cos_sin, cs + lane + half);
+        const float s1 = E::ld(cos_sin, cs + D + lane), s2 = E::ld(cos_sin, cs + D + lane + half);
+        y1 = E::rnd(E::rnd(a * c1) + E::rnd(-b * s1));
+        y2 = E::rnd(E::rnd(b * c2) + E::rnd(a * s2));
+    }
+    if (is_q) {
+        if (on) {
+            const size_t o = ((size_t)t * nq + j) * D;
+            E::st(q_out, o + lane, y1);
+            E::st(q_out, o + lane + half, y2);
+        }
+        return;
+    }
+    const size_t vcol = ((size_t)t * (nq + 2 * nkv) + nq + nkv + h) * D;
+    if (!INT8) {
+        const size_t dst = (size_t)row * D;
+        if (on) {
+            E::st(kp, dst + lane, y1);
+            E::st(kp, dst + lane + half, y2);
+        }
+        for (int i = lane; i < D; i += WAVE) vp[dst + i] = qkv[vcol + i];
+    } else {
+        const size_t half_q = (size_t)pages * nkv * P * D, half_s = (size_t)pages * nkv * P;
+        // Element i = lane + 64 jj of the vector for quantize_store: pair halves map to
+        // lane (first half) and lane + half; for D = 128 that is j = 0 and j = 1 of lane.
+        float x[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) x[jj] = 0.0f;
+        // Gather the rotated key into the element-major layout through LDS.
+        __shared__ float kv_tmp[512];
+        if (on) {
+            kv_tmp[lane] = __fdiv_rn(y1, smooth[lane]);
+            kv_tmp[lane + half] = __fdiv_rn(y2, smooth[lane + half]);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            const int i = lane + WAVE * jj;
+            if (i < D) x[jj] = kv_tmp[i];
+        }
+        quantize_store(x, D, lq, ls, (size_t)row);
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) {
+            const int i = lane + WAVE * jj;
+            x[jj] = i < D ? E::ld(qkv, vcol + i) : 0.0f;
+        }
+        quantize_store(x, D, lq + half_q, ls + half_s, (size_t)row);
+    }
+}
+
+}  // namespace
+
+int ti_launch_rope(int dtype, void *y, const void *x, const void *cos_t, const void *sin_t,
+                   int table_len, const int32_t *positions, int n, int heads, int D,
+                   hipStream_t s) {
+    dim3 grid((heads * (D / 2) + 255) / 256, n);
+    if (dtype == TI_BF16)
+        rope_kernel<uint16_t><<<grid, 256, 0, s>>>((uint16_t *)y, (const uint16_t *)x,
+                                                   (const uint16_t *)cos_t, (const uint16_t *)sin_t,
+                                                   table_len, positions, heads, D);
+    else
+        rope_kernel<float><<<grid, 256, 0, s>>>((float *)y, (const float *)x, (const float *)cos_t,
+                                                (const float *)sin_t, table_len, positions, heads, D);
+    return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
+}
+
+int ti_launch_store_kv(int dtype, const ti_kv_cache *c, const void *k, const void *v,
+                       const int32_t *slots, int n, hipStream_t s) {
+    dim3 grid(n, c->kv_heads);
+    const int D = c->head_dim, P = c->page_size, H = c->kv_heads, pages = c->num_pages;
+    if (c->kind == TI_KV_INT8) {
+        if (dtype == TI_BF16)
+            store_kv_int8_kernel<uint16_t><<<grid, 64, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
+                                                               (const uint16_t *)k, (const uint16_t *)v,
+                                                               slots, D, P, H, pages);
+        else
+            store_kv_int8_kernel<float><<<grid, 64, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
+                                                            (const float *)k, (const float *)v, slots,
+                                                            D, P, H, pages);
+    } else if (dtype == TI_BF16) {
+        store_kv_kernel<uint16_t><<<grid, 64, 0, s>>>((uint16_t *)c->k_pages, (uint16_t *)c->v_pages,
+                                                      (const uint16_t *)k, (const uint16_t *)v, slots,
+                                                      D, P, H, pages);
+    } else {
+        store_kv_kernel<float><<<grid, 64, 0, s>>>((float *)c->k_pages, (float *)c->v_pages,
+                                                   (const float *)k, (const float *)v, slots, D, P,
+                                                   H, pages);
+    }
+    return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
+}
+
+template <typename T, bool NORM, bool INT8>
+static void launch_inputs(void *q_out, const ti_kv_cache *c, const void *qkv, const void *q_norm,
+                          const void *k_norm, const void *cos_sin, int table_len,
+                          const int32_t *positions, const int32_t *slots, int n, int nq,
+                          float eps, hipStream_t s) {
+    dim3 grid(n, nq + c->kv_heads);
+    attention_inputs_kernel<T, NORM, INT8><<<grid, 64, 0, s>>>(
+        (T *)q_out, (T *)c->k_pages, (T *)c->v_pages, c->layer_q, c->layer_scale, c->smooth,
+        (const T *)qkv, (const T *)q_norm, (const T *)k_norm, (const T *)cos_sin, table_len,
+        positions, slots, nq, c->kv_heads, c->head_dim, c->page_size, c->num_pages, eps);
+}
+
+int ti_launch_attention_inputs(int dtype, void *q_out, const ti_kv_cache *c, const void *qkv,
+                               const void *q_norm, const void *k_norm, const void *cos_sin,
+                               int table_len, const int32_t *positions, const int32_t *slots,
+                               int n, int q_heads, float eps, hipStream_t s) {
+    const bool norm = q_norm != nullptr, int8 = c->kind == TI_KV_INT8;
+#define TI_INPUTS(T, N, I)                                                                        \
+    launch_inputs<T, N, I>(q_out, c, qkv, q_norm, k_norm, cos_sin, table_len, positions, slots, n, \
+                           q_heads, eps, s)
+    if (dtype == TI_BF16) {
+        if (norm) { if (int8) TI_INPUTS(uint16_t, true, true); else TI_INPUTS(uint16_t, true, false); }
+        else { if (int8) TI_INPUTS(uint16_t, false, true); else TI_INPUTS(uint16_t, false, false); }
+    } else {
+        if (norm) { if (int8) TI_INPUTS(float, true, true); else TI_INPUTS(float, true, false); }
+        else { if (int8) TI_INPUTS(float, false, true); else TI_INPUTS(float, false, false); }
+    }
+#undef TI_INPUTS
+    return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
+}
