@@ -25,6 +25,9 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # Packed FP32 (v_pk_*_f32) is off for every kernel: hipcc would otherwise form it.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs (not AGPRs): avoids per-tile AGPR<->VGPR copies around
+    # the online-softmax rescale.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"), "-I", CSRC,
     "-Wall", "-Wno-unused-function",
 ]

@@ -84,7 +84,7 @@ int ti_attention(const ti_attention_args *a, const ti_kv_cache *c, void *stream)
     if (path == 0) return ti_launch_generic(a, c, s);
     if (path == 2) return ti_launch_prefill(a, c, s);
     const ti_decode_plan pl = ti_plan_decode(a, c);
-    if (!a->workspace || a->workspace_bytes < pl.bytes) return TI_ERR_WORKSPACE;
+    if (pl.bytes > 0 && (!a->workspace || a->workspace_bytes < pl.bytes)) return TI_ERR_WORKSPACE;
     return ti_launch_decode(a, c, pl, s);
 }
 

@@ -93,6 +93,7 @@ int ti_launch_attention_inputs(int dtype, void *q_out, const ti_kv_cache *c, con
 
 struct ti_decode_plan {
     int splits;      // split-KV work-groups per (sequence, KV head)
+    int waves;       // waves per work-group (4 or 8)
     int rows;        // packed query rows G * max_query_len
     size_t bytes;    // workspace bytes
 };

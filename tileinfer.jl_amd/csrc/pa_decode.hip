@@ -30,6 +30,8 @@
 // At the end the four waves merge their (m, l, O) through LDS and the group writes one
 // Float32 partial (acc[D], m, l) per packed row; the combine kernel merges the splits:
 // w_s = exp2(m_s - max m), o = sum acc_s w_s / sum l_s w_s.
+#include <stdlib.h>
+
 #include "common.hpp"
 
 using namespace ti;
@@ -44,7 +46,7 @@ struct DecodeParams {
     const float *ls, *smooth;
     const int32_t *positions, *qsl, *bt;
     float *part;
-    int bt_stride, num_pages, P, Hk, Hq, G, nmax, M, splits, causal;
+    int bt_stride, num_pages, P, pshift, Hk, Hq, G, nmax, M, splits, causal;
     float scale_log2;
 };
 
@@ -52,6 +54,7 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // Transposed V tile in LDS: [D][16 keys] bf16, rows padded to 40 B (conflict-free reads).
 constexpr int VT_ROW = 20;  // uint16 per padded row
+constexpr float RESCALE_LOG2 = 8.0f;
 
 __device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
@@ -65,18 +68,90 @@ __device__ __forceinline__ u32x4 i8x8_to_bf16(uint2 v) {
     return r;
 }
 
-template <int D, int ROWB, bool INT8>
-__global__ void __launch_bounds__(256) decode_kernel(DecodeParams p) {
+// One 16-key tile's raw loads, held in registers from issue to use (software pipeline).
+template <int D, bool INT8>
+struct TileRegs {
+    static constexpr int NKB = D / 32;
+    static constexpr int KPL = 16 * (D / 8) / 64;
+    u32x4 k[NKB];          // dense: 8 bf16 per 32-wide block;   INT8: .xy = 8 int8
+    u32x4 v[KPL];          // dense: 8 bf16 of key vg*KPL + e;   INT8: .xy = 8 int8
+    float sk, sv;          // INT8 scales of this lane's K key
+};
+
+// Pool row of key position pos of KV head h. PG16: the 16-key tile lies in one page
+// (P % 16 == 0), so the caller passes the page's first row; otherwise a per-key lookup
+// with the position clamped into the sequence (rows past len are never used unmasked).
+struct RowMap {
+    const int32_t *bt;
+    int P, pshift, Hk, h, num_pages, len;
+    __device__ __forceinline__ int page_index(int pos) const {
+        return pshift >= 0 ? (pos >> pshift) : pos / P;
+    }
+    __device__ __forceinline__ int page_offset(int pos) const {
+        return pshift >= 0 ? (pos & (P - 1)) : pos % P;
+    }
+    __device__ __forceinline__ long long row(int pos) const {
+        pos = min(pos, len - 1);
+        const int pg = page_of(bt, page_index(pos), num_pages);
+        return ((long long)pg * Hk + h) * P + page_offset(pos);
+    }
+};
+
+template <int D, bool INT8, bool PG16>
+__device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodeParams &p,
+                                          const RowMap &rm, int j, int r16, int kg, int vg,
+                                          int vc, size_t half_q, size_t half_s) {
+    constexpr int NKB = TileRegs<D, INT8>::NKB, KPL = TileRegs<D, INT8>::KPL;
+    long long krow, vrow[KPL];
+    if (PG16) {
+        // One page per tile (wave-uniform); keys past len read the last valid key's row,
+        // whose finite values meet p = 0 (never stale memory that could hold NaN).
+        const long long r0 = rm.row(j * 16);
+        const int last = rm.len - 1 - j * 16;
+        krow = r0 + min(r16, last);
+#pragma unroll
+        for (int e = 0; e < KPL; e++) vrow[e] = r0 + min(vg * KPL + e, last);
+    } else {
+        krow = rm.row(j * 16 + r16);
+#pragma unroll
+        for (int e = 0; e < KPL; e++) vrow[e] = rm.row(j * 16 + vg * KPL + e);
+    }
+    if (!INT8) {
+#pragma unroll
+        for (int i = 0; i < NKB; i++)
+            t.k[i] = *reinterpret_cast<const u32x4 *>(p.kp + krow * D + i * 32 + kg * 8);
+#pragma unroll
+        for (int e = 0; e < KPL; e++)
+            t.v[e] = *reinterpret_cast<const u32x4 *>(p.vp + vrow[e] * D + vc * 8);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NKB; i++) {
+            const uint2 r = *reinterpret_cast<const uint2 *>(p.lq + krow * D + i * 32 + kg * 8);
+            t.k[i] = (u32x4){r.x, r.y, 0u, 0u};
+        }
+#pragma unroll
+        for (int e = 0; e < KPL; e++) {
+            const uint2 r = *reinterpret_cast<const uint2 *>(p.lq + half_q + vrow[e] * D + vc * 8);
+            t.v[e] = (u32x4){r.x, r.y, 0u, 0u};
+        }
+        t.sk = p.ls[krow];
+        t.sv = p.ls[half_s + krow];
+    }
+}
+
+template <int D, int ROWB, bool INT8, bool PG16, int NW>
+__global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     constexpr int NKB = D / 32;          // 32-wide head-dim blocks (QK MFMAs per tile)
     constexpr int NDT = D / 16;          // 16-wide head-dim tiles (PV MFMAs per tile)
     constexpr int CPR = D / 8;           // 8-element chunks per V row
     constexpr int KPL = 16 * CPR / 64;   // keys per lane in the V load (4 for D=128)
     constexpr int MP = ROWB * 16;        // padded rows
 
-    __shared__ __attribute__((aligned(16))) uint16_t vt[4][D * VT_ROW];
+    __shared__ __attribute__((aligned(16))) uint16_t vt[NW][D * VT_ROW];
     __shared__ float mrg[MP][D + 2];
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
     const int r16 = lane & 15, kg = lane >> 4;
     const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
@@ -86,9 +161,11 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeParams p) {
     const int ntiles = (len + 15) >> 4;
     const int per = (ntiles + p.splits - 1) / p.splits;
     const int j0 = s * per, j1 = min(j0 + per, ntiles);
-    const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
     const size_t half_q = (size_t)p.num_pages * p.Hk * p.P * D;
     const size_t half_s = (size_t)p.num_pages * p.Hk * p.P;
+    const RowMap rm{p.bt + (size_t)b * p.bt_stride, p.P, p.pshift, p.Hk, h, p.num_pages, len};
+    // Keys up to mask_from are visible to every row; later tiles need the mask.
+    const int mask_from = p.causal ? start : len - 1;
 
     // Query operands (B of S^T = K Q^T): row rb*16 + r16, elements i*32 + kg*8 .. +8.
     bf16x8 qreg[ROWB][NKB];
@@ -131,82 +208,50 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeParams p) {
     uint16_t *myvt = vt[w];
     const int vc = lane % CPR, vg = lane / CPR;   // V load: chunk, key group
 
-    for (int j = j0 + w; j < j1; j += 4) {
-        // ---- loads: K rows (lane key r16) and V rows (lane keys vg*KPL + e) ----
-        const int kpos = j * 16 + r16;
-        long long krow = -1;
-        if (kpos < len) {
-            const int pg = page_of(bt, kpos / p.P, p.num_pages);
-            krow = ((long long)pg * p.Hk + h) * p.P + kpos % p.P;
-        }
-        bf16x8 kreg[NKB];
-        float sk = 0.0f, sv = 0.0f;
-        if (!INT8) {
-#pragma unroll
-            for (int i = 0; i < NKB; i++)
-                kreg[i] = as_bf16x8(krow >= 0 ? *reinterpret_cast<const u32x4 *>(p.kp + krow * D + i * 32 + kg * 8)
-                                              : (u32x4){0u, 0u, 0u, 0u});
-        } else {
-#pragma unroll
-            for (int i = 0; i < NKB; i++) {
-                const uint2 raw = krow >= 0 ? *reinterpret_cast<const uint2 *>(p.lq + krow * D + i * 32 + kg * 8)
-                                            : make_uint2(0, 0);
-                kreg[i] = as_bf16x8(i8x8_to_bf16(raw));
-            }
-            if (krow >= 0) {
-                sk = p.ls[krow];
-                sv = p.ls[half_s + krow];
-            }
-        }
-        // V rows -> transposed LDS tile vt[d][key].
+    auto compute = [&](const TileRegs<D, INT8> &t, int j) {
+        // ---- V rows -> transposed LDS tile vt[d][key] ----
         {
-            uint32_t packed[8][KPL / 2];
-            uint16_t vals[KPL][8];
+            uint32_t words[KPL][4];
 #pragma unroll
             for (int e = 0; e < KPL; e++) {
-                const int key = vg * KPL + e, vpos = j * 16 + key;
-                if (vpos < len) {
-                    const int pg = page_of(bt, vpos / p.P, p.num_pages);
-                    const long long vrow = ((long long)pg * p.Hk + h) * p.P + vpos % p.P;
-                    if (!INT8) {
-                        const uint4 raw = *reinterpret_cast<const uint4 *>(p.vp + vrow * D + vc * 8);
-                        const uint32_t wds[4] = {raw.x, raw.y, raw.z, raw.w};
+                if (!INT8) {
 #pragma unroll
-                        for (int q2 = 0; q2 < 4; q2++) {
-                            vals[e][2 * q2] = (uint16_t)(wds[q2] & 0xffff);
-                            vals[e][2 * q2 + 1] = (uint16_t)(wds[q2] >> 16);
-                        }
-                    } else {
-                        const uint2 raw = *reinterpret_cast<const uint2 *>(p.lq + half_q + vrow * D + vc * 8);
-                        const u32x4 cv = i8x8_to_bf16(raw);
-#pragma unroll
-                        for (int q2 = 0; q2 < 4; q2++) {
-                            vals[e][2 * q2] = (uint16_t)(cv[q2] & 0xffff);
-                            vals[e][2 * q2 + 1] = (uint16_t)(cv[q2] >> 16);
-                        }
-                    }
+                    for (int q2 = 0; q2 < 4; q2++) words[e][q2] = t.v[e][q2];
                 } else {
-#pragma unroll
-                    for (int q2 = 0; q2 < 8; q2++) vals[e][q2] = 0;
+                    i8x4_to_bf16(t.v[e][0], words[e][0], words[e][1]);
+                    i8x4_to_bf16(t.v[e][1], words[e][2], words[e][3]);
                 }
             }
-#pragma unroll
-            for (int dd = 0; dd < 8; dd++)
-#pragma unroll
-                for (int e2 = 0; e2 < KPL / 2; e2++)
-                    packed[dd][e2] = (uint32_t)vals[2 * e2][dd] | ((uint32_t)vals[2 * e2 + 1][dd] << 16);
-            lds_fence();   // previous tile's reads of myvt are done before overwriting
+            lds_fence();   // the previous tile's reads of myvt are done before overwriting
 #pragma unroll
             for (int dd = 0; dd < 8; dd++) {
+                const int sh = (dd & 1) * 16;
                 uint16_t *dst = myvt + (vc * 8 + dd) * VT_ROW + vg * KPL;
-                if (KPL == 4)
-                    *reinterpret_cast<u32x2 *>(dst) = (u32x2){packed[dd][0], packed[dd][KPL / 2 - 1]};
-                else
-                    *reinterpret_cast<uint32_t *>(dst) = packed[dd][0];
+                if (KPL == 4) {
+                    const uint32_t w0 = __builtin_amdgcn_perm(words[1][dd / 2], words[0][dd / 2], sh ? 0x07060302u : 0x05040100u);
+                    const uint32_t w1 = __builtin_amdgcn_perm(words[3][dd / 2], words[2][dd / 2], sh ? 0x07060302u : 0x05040100u);
+                    *reinterpret_cast<u32x2 *>(dst) = (u32x2){w0, w1};
+                } else {
+                    *reinterpret_cast<uint32_t *>(dst) =
+                        __builtin_amdgcn_perm(words[1][dd / 2], words[0][dd / 2], sh ? 0x07060302u : 0x05040100u);
+                }
             }
         }
-
         // ---- S^T = K Q^T ----
+        bf16x8 kreg[NKB];
+#pragma unroll
+        for (int i = 0; i < NKB; i++) {
+            if (!INT8) {
+                kreg[i] = as_bf16x8(t.k[i]);
+            } else {
+                u32x4 wv;
+                uint32_t a0, a1, a2, a3;
+                i8x4_to_bf16(t.k[i][0], a0, a1);
+                i8x4_to_bf16(t.k[i][1], a2, a3);
+                wv[0] = a0; wv[1] = a1; wv[2] = a2; wv[3] = a3;
+                kreg[i] = as_bf16x8(wv);
+            }
+        }
         f32x4 sc[ROWB];
 #pragma unroll
         for (int rb = 0; rb < ROWB; rb++) {
@@ -215,68 +260,102 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeParams p) {
             for (int i = 0; i < NKB; i++)
                 sc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kreg[i], qreg[rb][i], sc[rb], 0, 0, 0);
         }
-        // Key scales of this lane's 4 keys (kg*4 + e), from the lanes that loaded them.
+        // Scales of this lane's 4 score keys (kg*4 + e), from the lanes that loaded them.
         float skk[4], svk[4];
         if (INT8) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                skk[e] = __shfl(sk, kg * 4 + e);
-                svk[e] = __shfl(sv, kg * 4 + e);
+                skk[e] = __shfl(t.sk, kg * 4 + e);
+                svk[e] = __shfl(t.sv, kg * 4 + e);
             }
         }
-
         // ---- online softmax + P^T operands ----
+        // Lazy rescaling: m is a reference max that only moves when a tile's max exceeds
+        // it by more than RESCALE_LOG2 (then p <= 2^RESCALE_LOG2, safe in bf16 and fp32);
+        // l and O always use the same reference, so the result is exact.
+        const bool need_mask = j * 16 + 15 > mask_from;
         s16x4 pop[ROWB];
-        float alpha[ROWB];
+        float x[ROWB][4], mt[ROWB];
+        bool grow = false;
 #pragma unroll
         for (int rb = 0; rb < ROWB; rb++) {
-            float x[4];
-            float mt = -INFINITY;
+            mt[rb] = -INFINITY;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const int kp = j * 16 + kg * 4 + e;
                 float v = sc[rb][e];
                 if (INT8) v *= skk[e];
                 v *= p.scale_log2;
-                x[e] = (kp <= qpos[rb] && kp < len) ? v : -INFINITY;
-                mt = fmaxf(mt, x[e]);
+                if (need_mask) {
+                    const int kp = j * 16 + kg * 4 + e;
+                    v = (kp <= qpos[rb] && kp < len) ? v : -INFINITY;
+                }
+                x[rb][e] = v;
+                mt[rb] = fmaxf(mt[rb], v);
             }
-            mt = fmaxf(mt, __shfl_xor(mt, 16));
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float mn = fmaxf(m[rb], mt);
-            alpha[rb] = fast_exp2(m[rb] - mn);
-            m[rb] = mn;
+            grow |= mt[rb] > m[rb] + RESCALE_LOG2;
+        }
+        if (__any(grow)) {
+#pragma unroll
+            for (int rb = 0; rb < ROWB; rb++) {
+                float t2 = fmaxf(mt[rb], __shfl_xor(mt[rb], 16));
+                t2 = fmaxf(t2, __shfl_xor(t2, 32));
+                const float mn = fmaxf(m[rb], t2);
+                const float alpha = fast_exp2(m[rb] - mn);
+                m[rb] = mn;
+                l[rb] *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) o[rb][dt] *= alpha;
+            }
+        }
+#pragma unroll
+        for (int rb = 0; rb < ROWB; rb++) {
             float ps = 0.0f, pe[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                pe[e] = fast_exp2(x[e] - mn);
+                pe[e] = fast_exp2(x[rb][e] - m[rb]);
                 ps += pe[e];
                 if (INT8) pe[e] *= svk[e];
             }
-            l[rb] = l[rb] * alpha[rb] + ps;
+            l[rb] += ps;
             pop[rb] = __builtin_bit_cast(s16x4, (u32x2){pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3])});
         }
-
-        // ---- O^T = alpha O^T + V^T P^T ----
+        // ---- O^T += V^T P^T ----
         lds_fence();   // this tile's V^T is in LDS
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
             const s16x4 a = __builtin_bit_cast(s16x4, *reinterpret_cast<const u32x2 *>(myvt + (dt * 16 + r16) * VT_ROW + kg * 4));
 #pragma unroll
-            for (int rb = 0; rb < ROWB; rb++) {
-                o[rb][dt] *= alpha[rb];
+            for (int rb = 0; rb < ROWB; rb++)
                 o[rb][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop[rb], o[rb][dt], 0, 0, 0);
-            }
+        }
+    };
+
+    // Two register sets, ping-ponged: tile j + NW is loading while tile j computes.
+    TileRegs<D, INT8> ta, tb;
+    int j = j0 + w;
+    if (j < j1) {
+        load_tile<D, INT8, PG16>(ta, p, rm, j, r16, kg, vg, vc, half_q, half_s);
+        while (true) {
+            const bool hb = j + NW < j1;
+            if (hb) load_tile<D, INT8, PG16>(tb, p, rm, j + NW, r16, kg, vg, vc, half_q, half_s);
+            compute(ta, j);
+            j += NW;
+            if (!hb) break;
+            const bool ha = j + NW < j1;
+            if (ha) load_tile<D, INT8, PG16>(ta, p, rm, j + NW, r16, kg, vg, vc, half_q, half_s);
+            compute(tb, j);
+            j += NW;
+            if (!ha) break;
         }
     }
 
-    // ---- merge the four waves' states through LDS (sequentially) ----
+    // ---- merge the waves' states through LDS (sequentially) ----
 #pragma unroll
     for (int rb = 0; rb < ROWB; rb++) {
         l[rb] += __shfl_xor(l[rb], 16);
         l[rb] += __shfl_xor(l[rb], 32);
     }
-    for (int src = 0; src < 4; src++) {
+    for (int src = 0; src < NW; src++) {
         if (w == src) {
 #pragma unroll
             for (int rb = 0; rb < ROWB; rb++) {
@@ -307,76 +386,151 @@ __global__ void __launch_bounds__(256) decode_kernel(DecodeParams p) {
         __syncthreads();
     }
 
+    if (p.splits == 1) {
+        // One split: this group saw every key, so normalize and write the output rows.
+        for (int idx = threadIdx.x; idx < p.M * D; idx += NW * 64) {
+            const int r = idx / D, d = idx - r * D, t = r / p.G, g = r - t * p.G;
+            if (t < nb)
+                p.out[((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D + d] = f2bf(mrg[r][d] / mrg[r][D + 1]);
+        }
+        return;
+    }
     // ---- write the partial of this split: part[unit][r][D + 2] for rows r < M ----
     const size_t unit = ((size_t)b * p.Hk + h) * p.splits + s;
     float *dst = p.part + unit * (size_t)p.M * (D + 2);
-    for (int idx = threadIdx.x; idx < p.M * (D + 2); idx += 256) {
+    for (int idx = threadIdx.x; idx < p.M * (D + 2); idx += NW * 64) {
         const int r = idx / (D + 2), c = idx - r * (D + 2);
         dst[idx] = mrg[r][c];
     }
 }
 
-// Merge the splits of one packed row: grid (M, Hk, B), one wave.
+// Merge the splits of one packed row: grid (M, Hk, B), 256 threads. The four waves take
+// every 4th split; lane owns head-dim elements lane + 64 k. Partials then meet in LDS.
 template <int D>
-__global__ void __launch_bounds__(64) combine_kernel(DecodeParams p) {
-    const int r = blockIdx.x, h = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+__global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
+    constexpr int PER = D / 64;
+    const int r = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
     const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
     const int t = r / p.G, g = r - t * p.G;
     if (t >= nb) return;
-    const size_t unit0 = ((size_t)b * p.Hk + h) * p.splits;
     const size_t stride = (size_t)p.M * (D + 2);
-    const float *base = p.part + unit0 * stride + (size_t)r * (D + 2);
+    const float *base = p.part + ((size_t)b * p.Hk + h) * p.splits * stride + (size_t)r * (D + 2);
     __shared__ float ws[256];
-    float mmax = NEG_BIG;
-    for (int sp = lane; sp < p.splits; sp += 64) mmax = fmaxf(mmax, base[sp * stride + D]);
-    mmax = wave_max(mmax);
-    float lsum = 0.0f;
-    for (int sp = lane; sp < p.splits; sp += 64) {
-        const float wgt = fast_exp2(base[sp * stride + D] - mmax);
-        ws[sp] = wgt;
-        lsum += base[sp * stride + D + 1] * wgt;
-    }
-    lsum = wave_sum(lsum);
+    __shared__ float red[4];
+    __shared__ float accs[4][D];
+    // global max of the splits' running maxima
+    float mx = NEG_BIG;
+    for (int sp = tid; sp < p.splits; sp += 256) mx = fmaxf(mx, base[sp * stride + D]);
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
     __syncthreads();
-    constexpr int PER = D / 64;
-    float acc[PER];
-#pragma unroll
-    for (int k = 0; k < PER; k++) acc[k] = 0.0f;
-    for (int sp = 0; sp < p.splits; sp++) {
-        const float wgt = ws[sp];
-#pragma unroll
-        for (int k = 0; k < PER; k++) acc[k] += base[sp * stride + lane + 64 * k] * wgt;
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    float ls = 0.0f;
+    for (int sp = tid; sp < p.splits; sp += 256) {
+        const float wgt = fast_exp2(base[sp * stride + D] - mx);
+        ws[sp] = wgt;
+        ls += base[sp * stride + D + 1] * wgt;
     }
-    uint16_t *o = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
+    ls = wave_sum(ls);
+    if (lane == 0) red[w] = ls;
+    __syncthreads();
+    ls = red[0] + red[1] + red[2] + red[3];
+    float acc[PER], acc2[PER];
 #pragma unroll
-    for (int k = 0; k < PER; k++) o[lane + 64 * k] = f2bf(acc[k] / lsum);
+    for (int k = 0; k < PER; k++) acc[k] = acc2[k] = 0.0f;
+    int sp = w;
+    for (; sp + 4 < p.splits; sp += 8) {
+        const float w0 = ws[sp], w1 = ws[sp + 4];
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            acc[k] += base[sp * stride + lane + 64 * k] * w0;
+            acc2[k] += base[(sp + 4) * stride + lane + 64 * k] * w1;
+        }
+    }
+    if (sp < p.splits) {
+        const float w0 = ws[sp];
+#pragma unroll
+        for (int k = 0; k < PER; k++) acc[k] += base[sp * stride + lane + 64 * k] * w0;
+    }
+#pragma unroll
+    for (int k = 0; k < PER; k++) accs[w][lane + 64 * k] = acc[k] + acc2[k];
+    __syncthreads();
+    if (w == 0) {
+        uint16_t *o = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
+        const float inv = 1.0f / ls;
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int d = lane + 64 * k;
+            o[d] = f2bf((accs[0][d] + accs[1][d] + accs[2][d] + accs[3][d]) * inv);
+        }
+    }
+}
+
+template <int D, bool INT8, bool PG16, int NW>
+void launch_decode_d(const DecodeParams &p, int rowb, dim3 grid, hipStream_t s) {
+    switch (rowb) {
+        case 1: decode_kernel<D, 1, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
+        case 2: decode_kernel<D, 2, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
+        case 3: decode_kernel<D, 3, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
+        default: decode_kernel<D, 4, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
+    }
 }
 
 template <int D, bool INT8>
-void launch_decode_d(const DecodeParams &p, int rowb, dim3 grid, hipStream_t s) {
-    switch (rowb) {
-        case 1: decode_kernel<D, 1, INT8><<<grid, 256, 0, s>>>(p); break;
-        case 2: decode_kernel<D, 2, INT8><<<grid, 256, 0, s>>>(p); break;
-        case 3: decode_kernel<D, 3, INT8><<<grid, 256, 0, s>>>(p); break;
-        default: decode_kernel<D, 4, INT8><<<grid, 256, 0, s>>>(p); break;
+void launch_decode_p(const DecodeParams &p, int rowb, int waves, dim3 grid, hipStream_t s) {
+    if (p.P % 16 == 0) {
+        if (waves == 8) launch_decode_d<D, INT8, true, 8>(p, rowb, grid, s);
+        else launch_decode_d<D, INT8, true, 4>(p, rowb, grid, s);
+    } else {
+        if (waves == 8) launch_decode_d<D, INT8, false, 8>(p, rowb, grid, s);
+        else launch_decode_d<D, INT8, false, 4>(p, rowb, grid, s);
     }
 }
 
 }  // namespace
 
-// Splits per (sequence, KV head): enough work-groups to fill 256 CUs several times over,
-// a power of two, depending only on host shapes (never on context length).
+// Work-groups per (sequence, KV head) and waves per group: about 8 waves per CU over the
+// 256 CUs. Large batches take one split of 8 waves per (sequence, KV head), which writes
+// the output directly (no partials, no combine launch); smaller ones split the keys into
+// a power of two of 4-wave groups (at most 32) merged by the combine kernel. Depends only
+// on host shapes, never on context length, so a captured graph stays valid.
 ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c) {
     ti_decode_plan pl;
     const int G = a->q_heads / c->kv_heads;
     pl.rows = G * a->max_query_len;
     const long long pairs = (long long)a->num_seqs * c->kv_heads;
-    const long long target = 2048;
-    int sp = 1;
-    while (sp < 128 && pairs * sp < target) sp <<= 1;
+    // TI_DECODE_TARGET_WGS / TI_DECODE_MAX_SPLITS / TI_DECODE_SPLITS / TI_DECODE_WAVES
+    // override the defaults (tuning only).
+    static const long long target = [] {
+        const char *e = getenv("TI_DECODE_TARGET_WGS");
+        return e ? atoll(e) : 512LL;
+    }();
+    static const int max_splits = [] {
+        const char *e = getenv("TI_DECODE_MAX_SPLITS");
+        return e ? atoi(e) : 32;
+    }();
+    static const int forced = [] {
+        const char *e = getenv("TI_DECODE_SPLITS");
+        return e ? atoi(e) : 0;
+    }();
+    static const int forced_waves = [] {
+        const char *e = getenv("TI_DECODE_WAVES");
+        return e ? atoi(e) : 0;
+    }();
+    int sp = 1, nw = 4;
+    if (pairs * 8 >= 2048) {
+        nw = 8;
+    } else {
+        while (sp < max_splits && pairs * sp < target) sp <<= 1;
+    }
+    if (forced > 0) sp = forced;
+    if (forced_waves == 4 || forced_waves == 8) nw = forced_waves;
     pl.splits = sp;
-    pl.bytes = (size_t)pairs * sp * pl.rows * (c->head_dim + 2) * sizeof(float);
+    pl.waves = nw;
+    pl.bytes = sp == 1 ? 0 : (size_t)pairs * sp * pl.rows * (c->head_dim + 2) * sizeof(float);
     return pl;
 }
 
@@ -397,6 +551,7 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
     p.bt_stride = a->block_table_stride;
     p.num_pages = c->num_pages;
     p.P = c->page_size;
+    p.pshift = (c->page_size & (c->page_size - 1)) == 0 ? __builtin_ctz(c->page_size) : -1;
     p.Hk = c->kv_heads;
     p.Hq = a->q_heads;
     p.G = a->q_heads / c->kv_heads;
@@ -409,15 +564,16 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
     dim3 grid(pl.splits, c->kv_heads, a->num_seqs);
     const bool int8 = c->kind == TI_KV_INT8;
     if (c->head_dim == 128) {
-        if (int8) launch_decode_d<128, true>(p, rowb, grid, s);
-        else launch_decode_d<128, false>(p, rowb, grid, s);
+        if (int8) launch_decode_p<128, true>(p, rowb, pl.waves, grid, s);
+        else launch_decode_p<128, false>(p, rowb, pl.waves, grid, s);
     } else {
-        if (int8) launch_decode_d<64, true>(p, rowb, grid, s);
-        else launch_decode_d<64, false>(p, rowb, grid, s);
+        if (int8) launch_decode_p<64, true>(p, rowb, pl.waves, grid, s);
+        else launch_decode_p<64, false>(p, rowb, pl.waves, grid, s);
     }
     if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
+    if (pl.splits == 1) return TI_OK;
     dim3 cgrid(pl.rows, c->kv_heads, a->num_seqs);
-    if (c->head_dim == 128) combine_kernel<128><<<cgrid, 64, 0, s>>>(p);
-    else combine_kernel<64><<<cgrid, 64, 0, s>>>(p);
+    if (c->head_dim == 128) combine_kernel<128><<<cgrid, 256, 0, s>>>(p);
+    else combine_kernel<64><<<cgrid, 256, 0, s>>>(p);
     return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
 }

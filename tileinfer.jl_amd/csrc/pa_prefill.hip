@@ -168,7 +168,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
     constexpr int NDT = D / 16;
     __shared__ __attribute__((aligned(16))) Smem<D> sm;
 
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
     const int r16 = lane & 15, kg = lane >> 4;
     const int qt = p.qtiles - 1 - (int)blockIdx.x;   // heaviest tiles first
     const int h = blockIdx.y, b = blockIdx.z;
