@@ -78,6 +78,18 @@ __device__ __forceinline__ int page_of(const int32_t *bt, int idx, int num_pages
     return p >= num_pages ? num_pages - 1 : p;
 }
 
+// The same lookup for a wave-uniform index, as a scalar load through the constant address
+// space: it is counted by lgkmcnt, so waiting for it never waits for the vector loads of
+// prefetched tiles (vmcnt is in order).
+__device__ __forceinline__ int page_of_s(const int32_t *bt, int idx, int num_pages) {
+    idx = __builtin_amdgcn_readfirstlane(idx);
+    const __attribute__((address_space(4))) int32_t *cbt =
+        (const __attribute__((address_space(4))) int32_t *)bt;
+    int p = cbt[idx] - 1;
+    p = p < 0 ? 0 : p;
+    return p >= num_pages ? num_pages - 1 : p;
+}
+
 }  // namespace ti
 
 // Launchers implemented per kernel file, dispatched by api.hip.

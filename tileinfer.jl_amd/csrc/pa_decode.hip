@@ -95,6 +95,12 @@ struct RowMap {
         const int pg = page_of(bt, page_index(pos), num_pages);
         return ((long long)pg * Hk + h) * P + page_offset(pos);
     }
+    // pos wave-uniform: scalar block-table load
+    __device__ __forceinline__ long long row_s(int pos) const {
+        pos = min(pos, len - 1);
+        const int pg = page_of_s(bt, page_index(pos), num_pages);
+        return ((long long)pg * Hk + h) * P + page_offset(pos);
+    }
 };
 
 template <int D, bool INT8, bool PG16>
@@ -106,7 +112,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodePara
     if (PG16) {
         // One page per tile (wave-uniform); keys past len read the last valid key's row,
         // whose finite values meet p = 0 (never stale memory that could hold NaN).
-        const long long r0 = rm.row(j * 16);
+        const long long r0 = rm.row_s(j * 16);
         const int last = rm.len - 1 - j * 16;
         krow = r0 + min(r16, last);
 #pragma unroll
@@ -330,22 +336,22 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
         }
     };
 
-    // Two register sets, ping-ponged: tile j + NW is loading while tile j computes.
+    // Two register sets, ping-ponged: tile j + NW is loading while tile j computes. The
+    // prefetch is issued unconditionally (past the last tile it re-reads that tile, unused)
+    // so the count of loads in flight is static and each wait covers only the tile in use.
     TileRegs<D, INT8> ta, tb;
     int j = j0 + w;
     if (j < j1) {
         load_tile<D, INT8, PG16>(ta, p, rm, j, r16, kg, vg, vc, half_q, half_s);
         while (true) {
-            const bool hb = j + NW < j1;
-            if (hb) load_tile<D, INT8, PG16>(tb, p, rm, j + NW, r16, kg, vg, vc, half_q, half_s);
+            load_tile<D, INT8, PG16>(tb, p, rm, min(j + NW, j1 - 1), r16, kg, vg, vc, half_q, half_s);
             compute(ta, j);
             j += NW;
-            if (!hb) break;
-            const bool ha = j + NW < j1;
-            if (ha) load_tile<D, INT8, PG16>(ta, p, rm, j + NW, r16, kg, vg, vc, half_q, half_s);
+            if (j >= j1) break;
+            load_tile<D, INT8, PG16>(ta, p, rm, min(j + NW, j1 - 1), r16, kg, vg, vc, half_q, half_s);
             compute(tb, j);
             j += NW;
-            if (!ha) break;
+            if (j >= j1) break;
         }
     }
 
