@@ -87,6 +87,19 @@ def decode_bytes(B, L, n, Hq, Hk, D, kv_elt_bytes):
     return B * (2 * L * Hk * kv_elt_bytes + 2 * n * Hq * D * 2)
 
 
+def measured_traffic():
+    """HBM bytes per headline launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (copy-calibrated), or None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "decode_b32_ctx4096_pmc.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(B, L, Hq, Hk, D, P, budget_s=10.0):
     """The oracle's Float32 eager op (src/ops/reference.jl:95-121) on the host cores over
     a sample of the headline workload, repeated for about budget_s seconds; the rate is
@@ -123,6 +136,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="", help="comma list: decode,prefill,int8,verify,kvwrite")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only copy a 512 MiB buffer 5 times (reference for rocprof byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, "
@@ -130,6 +145,14 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        src = torch.ones(256 << 20, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": src.numel() * 2}))
+        return
     import tileinfer_hip as ti
     ti.load_library()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -231,8 +254,10 @@ def main():
                    "global_batch": B, "context": L, "q_heads": Hq, "kv_heads": Hk, "head_dim": D,
                    "page_size": P, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "note": "event time of the whole call (decode + combine kernels)"},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "note": "achieved = algorithmic bytes per call / HIP-event time per call; the call is "
+                             "one decode_kernel launch (one split per sequence and KV head, no combine); "
+                             "traffic = rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, copy-calibrated"},
     }
     result.update(extra)
     if not args.no_cpu:
