@@ -153,8 +153,14 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     constexpr int KPL = 16 * CPR / 64;   // keys per lane in the V load (4 for D=128)
     constexpr int MP = ROWB * 16;        // padded rows
 
-    __shared__ __attribute__((aligned(16))) uint16_t vt[NW][D * VT_ROW];
-    __shared__ float mrg[MP][D + 2];
+    // Per-wave transposed V tiles during the key loop; afterwards the same LDS holds each
+    // wave's (O, m, l) slab for the merge (rows of D + 4 floats, 16-B aligned).
+    constexpr int MROW = D + 4;
+    constexpr int VT_BYTES = NW * D * VT_ROW * 2;
+    constexpr int SLAB_BYTES = NW * MP * MROW * 4;
+    __shared__ __attribute__((aligned(16))) char smem_raw[VT_BYTES > SLAB_BYTES ? VT_BYTES : SLAB_BYTES];
+    uint16_t (*vt)[D * VT_ROW] = reinterpret_cast<uint16_t (*)[D * VT_ROW]>(smem_raw);
+    float *mslab = reinterpret_cast<float *>(smem_raw);
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
@@ -355,58 +361,59 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
         }
     }
 
-    // ---- merge the waves' states through LDS (sequentially) ----
+    // ---- merge the waves' states (same rows, disjoint keys) through LDS slabs ----
 #pragma unroll
     for (int rb = 0; rb < ROWB; rb++) {
         l[rb] += __shfl_xor(l[rb], 16);
         l[rb] += __shfl_xor(l[rb], 32);
     }
-    for (int src = 0; src < NW; src++) {
-        if (w == src) {
+    __syncthreads();   // every wave is done with its V tile
 #pragma unroll
-            for (int rb = 0; rb < ROWB; rb++) {
-                const int r = rb * 16 + r16;
-                float mo = NEG_BIG, lo = 0.0f;
-                if (src > 0) {
-                    mo = mrg[r][D];
-                    lo = mrg[r][D + 1];
-                }
-                const float mn = fmaxf(mo, m[rb]);
-                const float wo = src > 0 ? fast_exp2(mo - mn) : 0.0f;
-                const float wm = fast_exp2(m[rb] - mn);
+    for (int rb = 0; rb < ROWB; rb++) {
+        float *my = mslab + ((size_t)w * MP + rb * 16 + r16) * MROW;
 #pragma unroll
-                for (int dt = 0; dt < NDT; dt++)
+        for (int dt = 0; dt < NDT; dt++)
+            *reinterpret_cast<f32x4 *>(my + dt * 16 + kg * 4) = o[rb][dt];
+        if (kg == 0) {
+            my[D] = m[rb];
+            my[D + 1] = l[rb];
+        }
+    }
+    __syncthreads();
+    const size_t unit = ((size_t)b * p.Hk + h) * p.splits + s;
+    for (int item = threadIdx.x; item < p.M * (D / 4); item += NW * 64) {
+        const int r = item / (D / 4), d4 = (item % (D / 4)) * 4;
+        float mx = NEG_BIG;
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int d = dt * 16 + kg * 4 + e;
-                        const float prev = src > 0 ? mrg[r][d] : 0.0f;
-                        mrg[r][d] = prev * wo + o[rb][dt][e] * wm;
-                    }
-                lds_fence();
-                if (kg == 0) {
-                    mrg[r][D] = mn;
-                    mrg[r][D + 1] = lo * wo + l[rb] * wm;
-                }
+        for (int wi = 0; wi < NW; wi++) mx = fmaxf(mx, mslab[((size_t)wi * MP + r) * MROW + D]);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        float lsum = 0.0f;
+#pragma unroll
+        for (int wi = 0; wi < NW; wi++) {
+            const float *src = mslab + ((size_t)wi * MP + r) * MROW;
+            const float wgt = fast_exp2(src[D] - mx);
+            lsum += src[D + 1] * wgt;
+            acc += *reinterpret_cast<const f32x4 *>(src + d4) * wgt;
+        }
+        if (p.splits == 1) {
+            // One split: this group saw every key; normalize and write the output rows.
+            const int t = r / p.G, g = r - t * p.G;
+            if (t < nb) {
+                const float inv = 1.0f / lsum;
+                uint16_t *o16 = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D + d4;
+                *reinterpret_cast<u32x2 *>(o16) = (u32x2){pack_bf16x2(acc[0] * inv, acc[1] * inv),
+                                                          pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+            }
+        } else {
+            // The split's partial: part[unit][r][D + 2] = (acc, m, l).
+            float *dst = p.part + (unit * (size_t)p.M + r) * (D + 2);
+#pragma unroll
+            for (int e = 0; e < 4; e++) dst[d4 + e] = acc[e];
+            if (d4 == 0) {
+                dst[D] = mx;
+                dst[D + 1] = lsum;
             }
         }
-        __syncthreads();
-    }
-
-    if (p.splits == 1) {
-        // One split: this group saw every key, so normalize and write the output rows.
-        for (int idx = threadIdx.x; idx < p.M * D; idx += NW * 64) {
-            const int r = idx / D, d = idx - r * D, t = r / p.G, g = r - t * p.G;
-            if (t < nb)
-                p.out[((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D + d] = f2bf(mrg[r][d] / mrg[r][D + 1]);
-        }
-        return;
-    }
-    // ---- write the partial of this split: part[unit][r][D + 2] for rows r < M ----
-    const size_t unit = ((size_t)b * p.Hk + h) * p.splits + s;
-    float *dst = p.part + unit * (size_t)p.M * (D + 2);
-    for (int idx = threadIdx.x; idx < p.M * (D + 2); idx += NW * 64) {
-        const int r = idx / (D + 2), c = idx - r * (D + 2);
-        dst[idx] = mrg[r][c];
     }
 }
 
@@ -477,11 +484,12 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
 
 template <int D, bool INT8, bool PG16, int NW>
 void launch_decode_d(const DecodeParams &p, int rowb, dim3 grid, hipStream_t s) {
+    // 8-wave groups only for up to 32 packed rows (their merge slabs must fit the LDS).
     switch (rowb) {
         case 1: decode_kernel<D, 1, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
         case 2: decode_kernel<D, 2, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
-        case 3: decode_kernel<D, 3, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
-        default: decode_kernel<D, 4, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
+        case 3: decode_kernel<D, 3, INT8, PG16, 4><<<grid, 4 * 64, 0, s>>>(p); break;
+        default: decode_kernel<D, 4, INT8, PG16, 4><<<grid, 4 * 64, 0, s>>>(p); break;
     }
 }
 
@@ -527,13 +535,13 @@ ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c) 
         return e ? atoi(e) : 0;
     }();
     int sp = 1, nw = 4;
-    if (pairs * 8 >= 2048) {
+    if (pairs * 8 >= 2048 && pl.rows <= 32) {
         nw = 8;
     } else {
         while (sp < max_splits && pairs * sp < target) sp <<= 1;
     }
     if (forced > 0) sp = forced;
-    if (forced_waves == 4 || forced_waves == 8) nw = forced_waves;
+    if ((forced_waves == 4 || forced_waves == 8) && pl.rows <= 32) nw = forced_waves;
     pl.splits = sp;
     pl.waves = nw;
     pl.bytes = sp == 1 ? 0 : (size_t)pairs * sp * pl.rows * (c->head_dim + 2) * sizeof(float);

@@ -46,32 +46,20 @@ struct PrefillParams {
 constexpr int KT = 32;                 // keys per LDS tile
 constexpr float RESCALE_LOG2 = 8.0f;   // lazy-rescale threshold (see the decode kernel)
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// One key group's LDS: K and V tiles row-major, double-buffered. Row strides (in bf16)
+// D + 8 for K (16-B reads by 16 consecutive lanes of 16 keys hit 64 distinct banks) and
+// D + 16 for V (the transposing reads of 4 rows x 32 B are bank-disjoint).
 template <int D>
 struct Smem {
-    static constexpr int KROW = D + 8;   // padded K row (uint16)
-    static constexpr int VROW = KT + 4;  // padded V^T row (uint16)
+    static constexpr int KROW = D + 8;
+    static constexpr int VROW = D + 16;
     uint16_t k[2][KT * KROW];
-    uint16_t vt[2][D * VROW];
+    uint16_t v[2][KT * VROW];
     float sk[2][KT], sv[2][KT];
 };
-
-// Registers holding one key tile between its global load and its LDS store (per thread
-// of a 256-thread key group).
-template <int D, bool INT8>
-struct Stage {
-    static constexpr int KCH = KT * D / 8;                    // 16 B (8-element) K chunks
-    static constexpr int KPT = (KCH + 255) / 256;             // K chunks per thread
-    uint4 k[KPT];          // bf16 K chunks (INT8: 8 bytes in .x/.y)
-    uint4 v[2];            // two V rows' chunk (key pair)
-    float s;               // a key or value scale (INT8)
-};
-
-__device__ __forceinline__ uint4 i8x8_to_bf16x8(uint2 v) {
-    uint4 r;
-    i8x4_to_bf16(v.x, r.x, r.y);
-    i8x4_to_bf16(v.y, r.z, r.w);
-    return r;
-}
 
 // Pool row of key position pos (clamped into the step's keys: rows past kend hold finite
 // cache data whose probabilities are masked to 0).
@@ -84,7 +72,7 @@ __device__ __forceinline__ long long key_row(const PrefillParams &p, const int32
     return ((long long)pg * p.Hk + h) * p.P + off;
 }
 
-// Rows of the tile's keys. PG16 (P % 16 == 0): each 16-key half of the tile lies in one
+// Rows of a tile's keys. PG16 (P % 16 == 0): each 16-key half of the tile lies in one
 // page, found with a scalar block-table load; key k's row is half_row[k / 16] + k % 16.
 // Otherwise a per-key lookup (vector loads).
 template <bool PG16>
@@ -116,37 +104,37 @@ struct TileRows {
     }
 };
 
-template <int D, bool INT8, bool PG16>
-__device__ __forceinline__ void load_tile(Stage<D, INT8> &st, const PrefillParams &p,
+// One tile's K and V (and INT8 scales) in registers between the global load and the LDS
+// store, for one thread of a GT-thread key group: chunk c = gtid + GT u of the tile's
+// KT x (D/8) 16-byte chunks (INT8: 8-byte chunks).
+template <int D, bool INT8, int GT>
+struct Stage {
+    static constexpr int CH = KT * D / 8;
+    static constexpr int PER = (CH + GT - 1) / GT;
+    u32x4 k[PER], v[PER];
+    float s;
+};
+
+template <int D, bool INT8, bool PG16, int GT>
+__device__ __forceinline__ void load_tile(Stage<D, INT8, GT> &st, const PrefillParams &p,
                                           const int32_t *bt, int h, int kt, int kend, int gtid) {
     const size_t half_q = (size_t)p.num_pages * p.Hk * p.P * D;
     const size_t half_s = (size_t)p.num_pages * p.Hk * p.P;
     constexpr int CPR = D / 8;
     const TileRows<PG16> tr(p, bt, h, kt, kend);
 #pragma unroll
-    for (int u = 0; u < Stage<D, INT8>::KPT; u++) {
-        const int c = gtid + 256 * u, key = c / CPR, ch = c % CPR;
-        if (c < Stage<D, INT8>::KCH) {
+    for (int u = 0; u < Stage<D, INT8, GT>::PER; u++) {
+        const int c = gtid + GT * u, key = c / CPR, ch = c % CPR;
+        if (c < Stage<D, INT8, GT>::CH) {
             const long long row = tr.row(key);
             if (!INT8) {
-                st.k[u] = *reinterpret_cast<const uint4 *>(p.kp + row * D + ch * 8);
+                st.k[u] = *reinterpret_cast<const u32x4 *>(p.kp + row * D + ch * 8);
+                st.v[u] = *reinterpret_cast<const u32x4 *>(p.vp + row * D + ch * 8);
             } else {
-                const uint2 raw = *reinterpret_cast<const uint2 *>(p.lq + row * D + ch * 8);
-                st.k[u] = make_uint4(raw.x, raw.y, 0, 0);
-            }
-        }
-    }
-    // V: unit = (key pair, chunk); KT/2 * CPR units (256 for D = 128).
-    const int kp2 = gtid / CPR, ch = gtid % CPR;
-    if (kp2 < KT / 2) {
-#pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const long long row = tr.row(2 * kp2 + e);
-            if (!INT8) {
-                st.v[e] = *reinterpret_cast<const uint4 *>(p.vp + row * D + ch * 8);
-            } else {
-                const uint2 raw = *reinterpret_cast<const uint2 *>(p.lq + half_q + row * D + ch * 8);
-                st.v[e] = make_uint4(raw.x, raw.y, 0, 0);
+                const uint2 a = *reinterpret_cast<const uint2 *>(p.lq + row * D + ch * 8);
+                const uint2 b = *reinterpret_cast<const uint2 *>(p.lq + half_q + row * D + ch * 8);
+                st.k[u] = (u32x4){a.x, a.y, 0u, 0u};
+                st.v[u] = (u32x4){b.x, b.y, 0u, 0u};
             }
         }
     }
@@ -156,29 +144,26 @@ __device__ __forceinline__ void load_tile(Stage<D, INT8> &st, const PrefillParam
     }
 }
 
-template <int D, bool INT8>
-__device__ __forceinline__ void store_tile(const Stage<D, INT8> &st, Smem<D> &sm, int buf, int gtid) {
+__device__ __forceinline__ u32x4 i8x8_to_bf16x8(uint32_t x, uint32_t y) {
+    u32x4 r;
+    uint32_t a, b, c, d;
+    i8x4_to_bf16(x, a, b);
+    i8x4_to_bf16(y, c, d);
+    r[0] = a; r[1] = b; r[2] = c; r[3] = d;
+    return r;
+}
+
+template <int D, bool INT8, int GT>
+__device__ __forceinline__ void store_tile(const Stage<D, INT8, GT> &st, Smem<D> &sm, int buf, int gtid) {
     constexpr int CPR = D / 8;
 #pragma unroll
-    for (int u = 0; u < Stage<D, INT8>::KPT; u++) {
-        const int c = gtid + 256 * u, key = c / CPR, ch = c % CPR;
-        if (c < Stage<D, INT8>::KCH) {
-            const uint4 val = INT8 ? i8x8_to_bf16x8(make_uint2(st.k[u].x, st.k[u].y)) : st.k[u];
-            *reinterpret_cast<uint4 *>(&sm.k[buf][key * Smem<D>::KROW + ch * 8]) = val;
-        }
-    }
-    const int kp2 = gtid / CPR, ch = gtid % CPR;
-    if (kp2 < KT / 2) {
-        uint4 a = st.v[0], b = st.v[1];
-        if (INT8) {
-            a = i8x8_to_bf16x8(make_uint2(a.x, a.y));
-            b = i8x8_to_bf16x8(make_uint2(b.x, b.y));
-        }
-        const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int dd = 0; dd < 8; dd++) {
-            const uint32_t word = __builtin_amdgcn_perm(wb[dd / 2], wa[dd / 2], (dd & 1) ? 0x07060302u : 0x05040100u);
-            *reinterpret_cast<uint32_t *>(&sm.vt[buf][(ch * 8 + dd) * Smem<D>::VROW + 2 * kp2]) = word;
+    for (int u = 0; u < Stage<D, INT8, GT>::PER; u++) {
+        const int c = gtid + GT * u, key = c / CPR, ch = c % CPR;
+        if (c < Stage<D, INT8, GT>::CH) {
+            const u32x4 kv = INT8 ? i8x8_to_bf16x8(st.k[u][0], st.k[u][1]) : st.k[u];
+            const u32x4 vv = INT8 ? i8x8_to_bf16x8(st.v[u][0], st.v[u][1]) : st.v[u];
+            *reinterpret_cast<u32x4 *>(&sm.k[buf][key * Smem<D>::KROW + ch * 8]) = kv;
+            *reinterpret_cast<u32x4 *>(&sm.v[buf][key * Smem<D>::VROW + ch * 8]) = vv;
         }
     }
     if (INT8 && gtid < 2 * KT) {
@@ -187,24 +172,43 @@ __device__ __forceinline__ void store_tile(const Stage<D, INT8> &st, Smem<D> &sm
     }
 }
 
-// NG key groups of 4 waves each. Every group holds all 64 packed rows (16 per wave) and
-// walks the key tiles kt = grp, grp + NG, ... with its own LDS double buffer and a
-// two-deep register prefetch, so NG tiles (and up to 2 NG more in flight) are processed at
-// once; the groups' online-softmax states merge through LDS at the end.
-template <int D, bool INT8, int NG, bool PG16>
-__global__ void __launch_bounds__(256 * NG) prefill_kernel(PrefillParams p) {
-    constexpr int NKB = D / 32;
-    constexpr int NDT = D / 16;
+__device__ __forceinline__ u32x2 lds_tr16(const uint16_t *p) {
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4 *)(__attribute__((address_space(3))) uint16_t *)p);
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// A work-group = NG key groups of WPG waves. Each wave owns 32 packed query rows
+// (row = g + G t, the G heads of one KV head times consecutive positions), so a group
+// covers 32 WPG rows; every group holds the same rows and walks the key tiles
+// kt = grp, grp + NG, ... through its own double-buffered LDS tiles with a two-deep
+// register prefetch; the groups' states merge through LDS at the end.
+//
+// Per wave and 32-key tile (lane l: row l % 32, k-group kg = l / 32):
+//   S^T = K Q^T     D/16 v_mfma_f32_32x32x16_bf16; A = K rows from LDS (16 B per lane),
+//                   B = Q^T in registers. Lane holds 16 scores of its row, keys
+//                   8 (e/4) + 4 kg + e%4.
+//   softmax         exp2 domain, lane-local, one xor-32 shuffle for the row max; lazy rescale.
+//   O^T += V^T P^T  2 x D/32 v_mfma_f32_32x32x16_bf16; B = P^T is the score registers
+//                   (keys 0-15, then 16-31), A = V^T built by ds_read_b64_tr_b16 from the
+//                   row-major V tile (two 8-B transposing reads per operand).
+template <int D, bool INT8, bool PG16, int WPG, int NG>
+__global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p) {
+    constexpr int NQB = D / 16;          // QK MFMAs (16 head-dim elements each)
+    constexpr int NDB = D / 32;          // 32-row output blocks of O^T
+    constexpr int GT = 64 * WPG;         // threads per key group
     constexpr int SMEM = sizeof(Smem<D>) * NG;
-    constexpr int MERGE = 64 * (D + 2) * 4;
+    constexpr int RPG = 32 * WPG;        // packed rows per group
+    constexpr int MROW = D + 4;          // merge slab row: O[D], m, l, pad (16-B aligned)
+    constexpr int MERGE = NG > 1 ? NG * RPG * MROW * 4 : 0;
     __shared__ __attribute__((aligned(16))) char smem_raw[SMEM > MERGE ? SMEM : MERGE];
     Smem<D> *smg = reinterpret_cast<Smem<D> *>(smem_raw);
-    float (*mrg)[D + 2] = reinterpret_cast<float (*)[D + 2]>(smem_raw);
+    float *mslab = reinterpret_cast<float *>(smem_raw);
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
-    const int grp = w >> 2, wl = w & 3, gtid = threadIdx.x & 255;
-    const int r16 = lane & 15, kg = lane >> 4;
+    const int grp = w / WPG, wl = w % WPG, gtid = threadIdx.x % GT;
+    const int r32 = lane & 31, kg = lane >> 5;
     // Grid (Hk, qtiles, B): consecutive work-groups (spread round-robin over the 8 XCDs)
     // belong to different KV heads, so each head's K/V stays in one XCD's L2.
     const int h = blockIdx.x;
@@ -221,19 +225,18 @@ __global__ void __launch_bounds__(256 * NG) prefill_kernel(PrefillParams p) {
     const int steps = (nkt + NG - 1) / NG;                 // same for every group
     const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
     Smem<D> &sm = smg[grp];
-    // Keys up to mask_from are visible to every row of this tile.
     const int mask_from = p.causal ? start + t_first : len - 1;
 
-    // This lane's query row (B operand of S^T = K Q^T).
-    const int r = wl * 16 + r16, tl = r / p.G, g = r - tl * p.G, t = t_first + tl;
+    // This lane's query row (B operand of S^T = K Q^T): elements i*16 + kg*8 .. +8.
+    const int r = wl * 32 + r32, tl = r / p.G, g = r - tl * p.G, t = t_first + tl;
     const bool row_ok = tl < p.TQ && t < nb;
     const int qpos = p.causal && row_ok ? start + t : len - 1;
-    bf16x8 qreg[NKB];
+    bf16x8 qreg[NQB];
     {
-        const uint16_t *qr = p.q + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
+        const uint16_t *qr = p.q + ((size_t)(tok0 + (row_ok ? t : 0)) * p.Hq + h * p.G + g) * D;
 #pragma unroll
-        for (int i = 0; i < NKB; i++) {
-            const int d0 = i * 32 + kg * 8;
+        for (int i = 0; i < NQB; i++) {
+            const int d0 = i * 16 + kg * 8;
             if (!row_ok) {
                 qreg[i] = as_bf16x8((u32x4){0u, 0u, 0u, 0u});
             } else if (!INT8) {
@@ -250,158 +253,174 @@ __global__ void __launch_bounds__(256 * NG) prefill_kernel(PrefillParams p) {
         }
     }
 
-    f32x4 o[NDT];
+    f32x16 o[NDB];
 #pragma unroll
-    for (int dt = 0; dt < NDT; dt++) o[dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < NDB; db++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[db][e] = 0.0f;
     float m = NEG_BIG, l = 0.0f;
 
+    // transposing-read address parts of this lane: 16-lane group c = lane / 16
+    const int c16 = lane >> 4, s16 = lane & 15;
+    const int tr_row = 4 * (c16 >> 1) + (s16 >> 2), tr_col = 16 * (c16 & 1) + 4 * (s16 & 3);
+
     auto compute = [&](int kt, int buf) {
-        f32x4 sc[2];
+        f32x16 sc;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            sc[kb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-            const uint16_t *krow = &sm.k[buf][(kb * 16 + r16) * Smem<D>::KROW];
+        for (int e = 0; e < 16; e++) sc[e] = 0.0f;
+        const uint16_t *krow = &sm.k[buf][r32 * Smem<D>::KROW + kg * 8];
 #pragma unroll
-            for (int i = 0; i < NKB; i++) {
-                const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + i * 32 + kg * 8));
-                sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qreg[i], sc[kb], 0, 0, 0);
-            }
+        for (int i = 0; i < NQB; i++) {
+            const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + i * 16));
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[i], sc, 0, 0, 0);
         }
         const bool need_mask = kt * KT + KT - 1 > mask_from;
-        float x[8];
+        float x[16];
         float mt = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int key = kb * 16 + kg * 4 + e;
-                float v = sc[kb][e];
-                if (INT8) v *= sm.sk[buf][key];
-                v *= p.scale_log2;
-                if (need_mask) {
-                    const int kpos = kt * KT + key;
-                    v = (kpos <= qpos && kpos < kend) ? v : -INFINITY;
-                }
-                x[kb * 4 + e] = v;
-                mt = fmaxf(mt, v);
+        for (int e = 0; e < 16; e++) {
+            const int key = 8 * (e >> 2) + 4 * kg + (e & 3);
+            float v = sc[e];
+            if (INT8) v *= sm.sk[buf][key];
+            v *= p.scale_log2;
+            if (need_mask) {
+                const int kpos = kt * KT + key;
+                v = (kpos <= qpos && kpos < kend) ? v : -INFINITY;
             }
+            x[e] = v;
+            mt = fmaxf(mt, v);
+        }
         if (__any(mt > m + RESCALE_LOG2)) {
-            mt = fmaxf(mt, __shfl_xor(mt, 16));
             mt = fmaxf(mt, __shfl_xor(mt, 32));
             const float mn = fmaxf(m, mt);
             const float alpha = fast_exp2(m - mn);
             m = mn;
             l *= alpha;
 #pragma unroll
-            for (int dt = 0; dt < NDT; dt++) o[dt] *= alpha;
+            for (int db = 0; db < NDB; db++) o[db] *= alpha;
         }
-        float ps = 0.0f, pe[8];
+        float pe[16], ps = 0.0f;
 #pragma unroll
-        for (int k8 = 0; k8 < 8; k8++) {
-            pe[k8] = fast_exp2(x[k8] - m);
-            ps += pe[k8];
-            if (INT8) pe[k8] *= sm.sv[buf][(k8 / 4) * 16 + kg * 4 + (k8 & 3)];
+        for (int e = 0; e < 16; e++) {
+            pe[e] = fast_exp2(x[e] - m);
+            ps += pe[e];
+            if (INT8) pe[e] *= sm.sv[buf][8 * (e >> 2) + 4 * kg + (e & 3)];
         }
-        const bf16x8 pb = as_bf16x8((u32x4){pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3]),
-                                            pack_bf16x2(pe[4], pe[5]), pack_bf16x2(pe[6], pe[7])});
         l += ps;
+        bf16x8 pb[2];
 #pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            const uint16_t *vrow = &sm.vt[buf][(dt * 16 + r16) * Smem<D>::VROW];
-            const u32x2 lo = *reinterpret_cast<const u32x2 *>(vrow + kg * 4);
-            const u32x2 hi = *reinterpret_cast<const u32x2 *>(vrow + 16 + kg * 4);
-            const bf16x8 a = as_bf16x8((u32x4){lo[0], lo[1], hi[0], hi[1]});
-            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[dt], 0, 0, 0);
-        }
+        for (int hh = 0; hh < 2; hh++)
+            pb[hh] = as_bf16x8((u32x4){pack_bf16x2(pe[8 * hh + 0], pe[8 * hh + 1]), pack_bf16x2(pe[8 * hh + 2], pe[8 * hh + 3]),
+                                       pack_bf16x2(pe[8 * hh + 4], pe[8 * hh + 5]), pack_bf16x2(pe[8 * hh + 6], pe[8 * hh + 7])});
+        const uint16_t *vb = &sm.v[buf][tr_row * Smem<D>::VROW + tr_col];
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const u32x2 lo = lds_tr16(vb + (16 * hh) * Smem<D>::VROW + 32 * db);
+                const u32x2 hi = lds_tr16(vb + (16 * hh + 8) * Smem<D>::VROW + 32 * db);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8((u32x4){lo[0], lo[1], hi[0], hi[1]}),
+                                                               pb[hh], o[db], 0, 0, 0);
+            }
     };
 
-    // Step i of this group handles tile grp + NG i. Register stages s0/s1 alternate: at
-    // step i, tile i + 1 is already in flight and tile i + 2 is issued.
     // Loads are issued unconditionally (a step past the group's last tile re-reads its
     // last tile, never used) so the number of loads in flight is static and the waits
     // before each LDS store only cover the tile being stored.
-    Stage<D, INT8> s0, s1;
+    Stage<D, INT8, GT> s0, s1;
     auto tile_of = [&](int i) { return grp + NG * i; };
-    auto ld = [&](Stage<D, INT8> &stg, int i) {
-        load_tile<D, INT8, PG16>(stg, p, bt, h, min(tile_of(i), nkt - 1), kend, gtid);
+    auto ld = [&](Stage<D, INT8, GT> &stg, int i) {
+        load_tile<D, INT8, PG16, GT>(stg, p, bt, h, min(tile_of(i), nkt - 1), kend, gtid);
     };
     ld(s0, 0);
     ld(s1, 1);
-    if (tile_of(0) < nkt) store_tile<D, INT8>(s0, sm, 0, gtid);
+    if (tile_of(0) < nkt) store_tile<D, INT8, GT>(s0, sm, 0, gtid);
     __syncthreads();
     for (int i = 0; i < steps; i += 2) {
-        // even step: compute buf 0, prefetch into s0, stage s1 -> buf 1
         ld(s0, i + 2);
         if (tile_of(i) < nkt) compute(tile_of(i), 0);
-        if (tile_of(i + 1) < nkt) store_tile<D, INT8>(s1, sm, 1, gtid);
+        if (tile_of(i + 1) < nkt) store_tile<D, INT8, GT>(s1, sm, 1, gtid);
         __syncthreads();
         if (i + 1 >= steps) break;
-        // odd step: compute buf 1, prefetch into s1, stage s0 -> buf 0
         ld(s1, i + 3);
         if (tile_of(i + 1) < nkt) compute(tile_of(i + 1), 1);
-        if (tile_of(i + 2) < nkt) store_tile<D, INT8>(s0, sm, 0, gtid);
+        if (tile_of(i + 2) < nkt) store_tile<D, INT8, GT>(s0, sm, 0, gtid);
         __syncthreads();
     }
 
-    l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     if (NG > 1) {
-        // Merge the groups' states (same rows, disjoint keys) through LDS, group by group.
-        for (int src = 0; src < NG; src++) {
-            if (grp == src) {
-                float mo = NEG_BIG, lo = 0.0f;
-                if (src > 0) {
-                    mo = mrg[r][D];
-                    lo = mrg[r][D + 1];
-                }
-                const float mn = fmaxf(mo, m);
-                const float wo = src > 0 ? fast_exp2(mo - mn) : 0.0f;
-                const float wm = fast_exp2(m - mn);
+        // Merge the groups' states (same rows, disjoint keys): every group writes its
+        // (O, m, l) to its own LDS slab, then all threads combine (row, 4 elements) items.
+        float *my = mslab + (size_t)grp * RPG * MROW + r * MROW;
 #pragma unroll
-                for (int dt = 0; dt < NDT; dt++)
+        for (int db = 0; db < NDB; db++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        const int d = dt * 16 + kg * 4 + e;
-                        const float prev = src > 0 ? mrg[r][d] : 0.0f;
-                        o[dt][e] = prev * wo + o[dt][e] * wm;
-                        mrg[r][d] = o[dt][e];
-                    }
-                l = lo * wo + l * wm;
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                if (kg == 0) {
-                    mrg[r][D] = mn;
-                    mrg[r][D + 1] = l;
-                }
-            }
-            __syncthreads();
+            for (int e4 = 0; e4 < 4; e4++)
+                *reinterpret_cast<f32x4 *>(my + 32 * db + 8 * e4 + 4 * kg) =
+                    (f32x4){o[db][4 * e4], o[db][4 * e4 + 1], o[db][4 * e4 + 2], o[db][4 * e4 + 3]};
+        if (kg == 0) {
+            my[D] = m;
+            my[D + 1] = l;
         }
-        if (grp != NG - 1) return;   // the last group holds the merged state in registers
+        __syncthreads();
+        for (int item = threadIdx.x; item < RPG * (D / 4); item += 64 * WPG * NG) {
+            const int rr = item / (D / 4), d4 = (item % (D / 4)) * 4;
+            const int ttl = rr / p.G, gg = rr - ttl * p.G, tt = t_first + ttl;
+            if (ttl >= p.TQ || tt >= nb) continue;
+            float mx = NEG_BIG;
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) mx = fmaxf(mx, mslab[((size_t)gi * RPG + rr) * MROW + D]);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            float lsum = 0.0f;
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                const float *src = mslab + ((size_t)gi * RPG + rr) * MROW;
+                const float wgt = fast_exp2(src[D] - mx);
+                lsum += src[D + 1] * wgt;
+                acc += *reinterpret_cast<const f32x4 *>(src + d4) * wgt;
+            }
+            const float inv = 1.0f / lsum;
+            uint16_t *orow = p.out + ((size_t)(tok0 + tt) * p.Hq + h * p.G + gg) * D + d4;
+            *reinterpret_cast<u32x2 *>(orow) = (u32x2){pack_bf16x2(acc[0] * inv, acc[1] * inv),
+                                                       pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+        }
+        return;
     }
     if (!row_ok) return;
     const float inv = 1.0f / l;
     uint16_t *orow = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
 #pragma unroll
-    for (int dt = 0; dt < NDT; dt++) {
-        const int d = dt * 16 + kg * 4;
-        const uint32_t w0 = pack_bf16x2(o[dt][0] * inv, o[dt][1] * inv);
-        const uint32_t w1 = pack_bf16x2(o[dt][2] * inv, o[dt][3] * inv);
-        *reinterpret_cast<u32x2 *>(orow + d) = (u32x2){w0, w1};
-    }
+    for (int db = 0; db < NDB; db++)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; e4++) {
+            const int d = 32 * db + 8 * e4 + 4 * kg;
+            const uint32_t w0 = pack_bf16x2(o[db][4 * e4 + 0] * inv, o[db][4 * e4 + 1] * inv);
+            const uint32_t w1 = pack_bf16x2(o[db][4 * e4 + 2] * inv, o[db][4 * e4 + 3] * inv);
+            *reinterpret_cast<u32x2 *>(orow + d) = (u32x2){w0, w1};
+        }
 }
 
 template <int D, bool INT8, bool PG16>
-void launch_prefill_g(const PrefillParams &p, int ng, dim3 grid, hipStream_t s) {
-    switch (ng) {
-        case 1: prefill_kernel<D, INT8, 1, PG16><<<grid, 256, 0, s>>>(p); break;
-        case 2: prefill_kernel<D, INT8, 2, PG16><<<grid, 512, 0, s>>>(p); break;
-        default: prefill_kernel<D, INT8, 4, PG16><<<grid, 1024, 0, s>>>(p); break;
+void launch_prefill_g(const PrefillParams &p, int wpg, int ng, dim3 grid, hipStream_t s) {
+    if (wpg == 2) {
+        switch (ng) {
+            case 1: prefill_kernel<D, INT8, PG16, 2, 1><<<grid, 128, 0, s>>>(p); break;
+            case 2: prefill_kernel<D, INT8, PG16, 2, 2><<<grid, 256, 0, s>>>(p); break;
+            default: prefill_kernel<D, INT8, PG16, 2, 4><<<grid, 512, 0, s>>>(p); break;
+        }
+    } else {
+        switch (ng) {
+            case 1: prefill_kernel<D, INT8, PG16, 4, 1><<<grid, 256, 0, s>>>(p); break;
+            default: prefill_kernel<D, INT8, PG16, 4, 2><<<grid, 512, 0, s>>>(p); break;
+        }
     }
 }
 
 template <int D, bool INT8>
-void launch_prefill_d(const PrefillParams &p, int ng, dim3 grid, hipStream_t s) {
-    if (p.P % 16 == 0) launch_prefill_g<D, INT8, true>(p, ng, grid, s);
-    else launch_prefill_g<D, INT8, false>(p, ng, grid, s);
+void launch_prefill_d(const PrefillParams &p, int wpg, int ng, dim3 grid, hipStream_t s) {
+    if (p.P % 16 == 0) launch_prefill_g<D, INT8, true>(p, wpg, ng, grid, s);
+    else launch_prefill_g<D, INT8, false>(p, wpg, ng, grid, s);
 }
 
 }  // namespace
@@ -425,28 +444,38 @@ int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, hipStrea
     p.Hk = c->kv_heads;
     p.Hq = a->q_heads;
     p.G = a->q_heads / c->kv_heads;
-    p.TQ = 64 / p.G;
     p.nmax = a->max_query_len;
-    p.qtiles = (a->max_query_len + p.TQ - 1) / p.TQ;
     p.causal = a->causal;
     p.scale_log2 = a->scale * LOG2E;
-    // Key groups per work-group: enough waves to hide the tile loads' latency when the
-    // grid alone cannot (TI_PREFILL_GROUPS overrides, tuning only).
-    static const int forced = [] {
+    // Shape: WPG waves (32 packed rows each) per key group and NG key groups per
+    // work-group, chosen so small prefills still spread over the 256 CUs
+    // (TI_PREFILL_WPG / TI_PREFILL_GROUPS override, tuning only).
+    static const int forced_wpg = [] {
+        const char *e = getenv("TI_PREFILL_WPG");
+        return e ? atoi(e) : 0;
+    }();
+    static const int forced_ng = [] {
         const char *e = getenv("TI_PREFILL_GROUPS");
         return e ? atoi(e) : 0;
     }();
+    const int G = p.G;
+    int wpg = G <= 64 && (long long)((a->max_query_len + 128 / G - 1) / (128 / G)) * c->kv_heads * a->num_seqs >= 256 ? 4 : 2;
+    if (forced_wpg == 2 || forced_wpg == 4) wpg = forced_wpg;
+    if (32 * wpg < G) wpg = 4;
+    p.TQ = 32 * wpg / G;
+    p.qtiles = (a->max_query_len + p.TQ - 1) / p.TQ;
     const long long wgs = (long long)p.qtiles * c->kv_heads * a->num_seqs;
     int ng = wgs >= 1024 ? 1 : (wgs >= 512 ? 2 : 4);
-    if (forced == 1 || forced == 2 || forced == 4) ng = forced;
+    if (forced_ng == 1 || forced_ng == 2 || forced_ng == 4) ng = forced_ng;
+    if (wpg == 4 && ng > 2) ng = 2;   // 16 waves of this kernel do not fit one CU's registers
     dim3 grid(c->kv_heads, p.qtiles, a->num_seqs);
     const bool int8 = c->kind == TI_KV_INT8;
     if (c->head_dim == 128) {
-        if (int8) launch_prefill_d<128, true>(p, ng, grid, s);
-        else launch_prefill_d<128, false>(p, ng, grid, s);
+        if (int8) launch_prefill_d<128, true>(p, wpg, ng, grid, s);
+        else launch_prefill_d<128, false>(p, wpg, ng, grid, s);
     } else {
-        if (int8) launch_prefill_d<64, true>(p, ng, grid, s);
-        else launch_prefill_d<64, false>(p, ng, grid, s);
+        if (int8) launch_prefill_d<64, true>(p, wpg, ng, grid, s);
+        else launch_prefill_d<64, false>(p, wpg, ng, grid, s);
     }
     return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
 }
