@@ -115,12 +115,64 @@ struct Stage {
     float s;
 };
 
+// Page ids (0-based, clamped into the pool) of the two 16-key halves of tile kt, read with
+// scalar loads; fetched one tile ahead of use so their latency hides behind compute.
+struct TilePages {
+    int pg[2];
+};
+
+__device__ __forceinline__ TilePages tile_pages(const PrefillParams &p, const int32_t *bt, int kt) {
+    TilePages tp;
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+        const int pos = kt * KT + 16 * x;
+        const int idx = min(p.pshift >= 0 ? pos >> p.pshift : pos / p.P, p.bt_stride - 1);
+        tp.pg[x] = page_of_s(bt, idx, p.num_pages);
+    }
+    return tp;
+}
+
 template <int D, bool INT8, bool PG16, int GT>
 __device__ __forceinline__ void load_tile(Stage<D, INT8, GT> &st, const PrefillParams &p,
-                                          const int32_t *bt, int h, int kt, int kend, int gtid) {
+                                          const int32_t *bt, int h, int kt, int kend, int gtid,
+                                          const TilePages &tp) {
     const size_t half_q = (size_t)p.num_pages * p.Hk * p.P * D;
     const size_t half_s = (size_t)p.num_pages * p.Hk * p.P;
     constexpr int CPR = D / 8;
+    constexpr int KPU = GT / CPR;              // keys covered by one chunk round (GT % CPR == 0)
+    if (PG16) {
+        // Each 16-key half of the tile lies in one page: the page's row base is scalar and
+        // chunk u of this thread sits at a loop-invariant offset from it. Keys past kend
+        // read stale-but-allocated rows of the same page (their scores are masked and their
+        // values zeroed when the tile is stored).
+        long long base[2];
+#pragma unroll
+        for (int x = 0; x < 2; x++) {
+            const int pos = kt * KT + 16 * x;
+            const int off = p.pshift >= 0 ? pos & (p.P - 1) : pos % p.P;
+            base[x] = (((long long)tp.pg[x] * p.Hk + h) * p.P + off) * D;
+        }
+#pragma unroll
+        for (int u = 0; u < Stage<D, INT8, GT>::PER; u++) {
+            const int key = gtid / CPR + KPU * u, ch = gtid % CPR;
+            const long long e0 = base[key >> 4] + (key & 15) * D + ch * 8;   // key >> 4 folds per u
+            if (!INT8) {
+                st.k[u] = *reinterpret_cast<const u32x4 *>(p.kp + e0);
+                st.v[u] = *reinterpret_cast<const u32x4 *>(p.vp + e0);
+            } else {
+                const uint2 a = *reinterpret_cast<const uint2 *>(p.lq + e0);
+                const uint2 b = *reinterpret_cast<const uint2 *>(p.lq + half_q + e0);
+                st.k[u] = (u32x4){a.x, a.y, 0u, 0u};
+                st.v[u] = (u32x4){b.x, b.y, 0u, 0u};
+            }
+        }
+        if (INT8 && gtid < 2 * KT) {
+            const int key = gtid % KT;
+            const long long row = base[key >> 4] / D + (key & 15);
+            st.s = gtid < KT ? p.ls[row] : p.ls[half_s + row];
+        }
+        return;
+    }
     const TileRows<PG16> tr(p, bt, h, kt, kend);
 #pragma unroll
     for (int u = 0; u < Stage<D, INT8, GT>::PER; u++) {
@@ -154,14 +206,17 @@ __device__ __forceinline__ u32x4 i8x8_to_bf16x8(uint32_t x, uint32_t y) {
 }
 
 template <int D, bool INT8, int GT>
-__device__ __forceinline__ void store_tile(const Stage<D, INT8, GT> &st, Smem<D> &sm, int buf, int gtid) {
+__device__ __forceinline__ void store_tile(const Stage<D, INT8, GT> &st, Smem<D> &sm, int buf, int gtid,
+                                           int valid_keys) {
     constexpr int CPR = D / 8;
+    const bool partial = valid_keys < KT;      // wave-uniform: only the last tile
 #pragma unroll
     for (int u = 0; u < Stage<D, INT8, GT>::PER; u++) {
         const int c = gtid + GT * u, key = c / CPR, ch = c % CPR;
         if (c < Stage<D, INT8, GT>::CH) {
             const u32x4 kv = INT8 ? i8x8_to_bf16x8(st.k[u][0], st.k[u][1]) : st.k[u];
-            const u32x4 vv = INT8 ? i8x8_to_bf16x8(st.v[u][0], st.v[u][1]) : st.v[u];
+            u32x4 vv = INT8 ? i8x8_to_bf16x8(st.v[u][0], st.v[u][1]) : st.v[u];
+            if (partial && key >= valid_keys) vv = (u32x4){0u, 0u, 0u, 0u};   // p = 0 meets 0
             *reinterpret_cast<u32x4 *>(&sm.k[buf][key * Smem<D>::KROW + ch * 8]) = kv;
             *reinterpret_cast<u32x4 *>(&sm.v[buf][key * Smem<D>::VROW + ch * 8]) = vv;
         }
@@ -265,15 +320,22 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     const int tr_row = 4 * (c16 >> 1) + (s16 >> 2), tr_col = 16 * (c16 & 1) + 4 * (s16 & 3);
 
     auto compute = [&](int kt, int buf) {
-        f32x16 sc;
+        // Two independent accumulation chains (even / odd head-dim blocks) halve the
+        // dependent-MFMA latency of the score tile.
+        f32x16 sc, sc2;
 #pragma unroll
-        for (int e = 0; e < 16; e++) sc[e] = 0.0f;
+        for (int e = 0; e < 16; e++) sc[e] = sc2[e] = 0.0f;
         const uint16_t *krow = &sm.k[buf][r32 * Smem<D>::KROW + kg * 8];
 #pragma unroll
-        for (int i = 0; i < NQB; i++) {
-            const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + i * 16));
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qreg[i], sc, 0, 0, 0);
+        for (int i = 0; i < NQB; i += 2) {
+            const bf16x8 a0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + i * 16));
+            const bf16x8 a1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + (i + 1) * 16));
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qreg[i], sc, 0, 0, 0);
+            sc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qreg[i + 1], sc2, 0, 0, 0);
         }
+        sc += sc2;
+        // Online softmax in the exp2 domain: p = exp2(s * scale - m) with m the running
+        // (scaled) reference max; the tile max is taken on raw scores (scale > 0).
         const bool need_mask = kt * KT + KT - 1 > mask_from;
         float x[16];
         float mt = -INFINITY;
@@ -282,7 +344,6 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
             const int key = 8 * (e >> 2) + 4 * kg + (e & 3);
             float v = sc[e];
             if (INT8) v *= sm.sk[buf][key];
-            v *= p.scale_log2;
             if (need_mask) {
                 const int kpos = kt * KT + key;
                 v = (kpos <= qpos && kpos < kend) ? v : -INFINITY;
@@ -290,6 +351,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
             x[e] = v;
             mt = fmaxf(mt, v);
         }
+        mt *= p.scale_log2;
         if (__any(mt > m + RESCALE_LOG2)) {
             mt = fmaxf(mt, __shfl_xor(mt, 32));
             const float mn = fmaxf(m, mt);
@@ -302,7 +364,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         float pe[16], ps = 0.0f;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-            pe[e] = fast_exp2(x[e] - m);
+            pe[e] = fast_exp2(__builtin_fmaf(x[e], p.scale_log2, -m));
             ps += pe[e];
             if (INT8) pe[e] *= sm.sv[buf][8 * (e >> 2) + 4 * kg + (e & 3)];
         }
@@ -329,22 +391,25 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     // before each LDS store only cover the tile being stored.
     Stage<D, INT8, GT> s0, s1;
     auto tile_of = [&](int i) { return grp + NG * i; };
+    // Page ids of the next tile to load, fetched one load ahead.
+    TilePages pnext = PG16 ? tile_pages(p, bt, min(tile_of(0), nkt - 1)) : TilePages{};
     auto ld = [&](Stage<D, INT8, GT> &stg, int i) {
-        load_tile<D, INT8, PG16, GT>(stg, p, bt, h, min(tile_of(i), nkt - 1), kend, gtid);
+        load_tile<D, INT8, PG16, GT>(stg, p, bt, h, min(tile_of(i), nkt - 1), kend, gtid, pnext);
+        if (PG16) pnext = tile_pages(p, bt, min(tile_of(i + 1), nkt - 1));
     };
     ld(s0, 0);
     ld(s1, 1);
-    if (tile_of(0) < nkt) store_tile<D, INT8, GT>(s0, sm, 0, gtid);
+    if (tile_of(0) < nkt) store_tile<D, INT8, GT>(s0, sm, 0, gtid, kend - tile_of(0) * KT);
     __syncthreads();
     for (int i = 0; i < steps; i += 2) {
         ld(s0, i + 2);
         if (tile_of(i) < nkt) compute(tile_of(i), 0);
-        if (tile_of(i + 1) < nkt) store_tile<D, INT8, GT>(s1, sm, 1, gtid);
+        if (tile_of(i + 1) < nkt) store_tile<D, INT8, GT>(s1, sm, 1, gtid, kend - tile_of(i + 1) * KT);
         __syncthreads();
         if (i + 1 >= steps) break;
         ld(s1, i + 3);
         if (tile_of(i + 1) < nkt) compute(tile_of(i + 1), 1);
-        if (tile_of(i + 2) < nkt) store_tile<D, INT8, GT>(s0, sm, 0, gtid);
+        if (tile_of(i + 2) < nkt) store_tile<D, INT8, GT>(s0, sm, 0, gtid, kend - tile_of(i + 2) * KT);
         __syncthreads();
     }
 
