@@ -42,9 +42,13 @@ template <> struct Elt<uint16_t> {
     static __device__ __forceinline__ void st(uint16_t *p, size_t i, float x) { p[i] = f2bf(x); }
 };
 
-// Two floats -> one word of two bf16 (round to nearest even), low element first.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Two floats -> one word of two bf16 (round to nearest even), low element first: one
+// v_cvt_pk_bf16_f32 (a whole-vector conversion, never element inserts).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
 }
 
 // MFMA operands are assembled from 32-bit words and bit-cast whole; building bf16

@@ -108,20 +108,47 @@ __device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodePara
                                           const RowMap &rm, int j, int r16, int kg, int vg,
                                           int vc, size_t half_q, size_t half_s) {
     constexpr int NKB = TileRegs<D, INT8>::NKB, KPL = TileRegs<D, INT8>::KPL;
-    long long krow, vrow[KPL];
     if (PG16) {
-        // One page per tile (wave-uniform); keys past len read the last valid key's row,
-        // whose finite values meet p = 0 (never stale memory that could hold NaN).
+        // One page per tile: a wave-uniform 64-bit base plus small per-lane 32-bit offsets
+        // (scalar-base addressing, no 64-bit vector math). Keys past len read the last
+        // valid key's row, whose finite values meet p = 0 (never stale memory that could
+        // hold NaN).
         const long long r0 = rm.row_s(j * 16);
         const int last = rm.len - 1 - j * 16;
-        krow = r0 + min(r16, last);
+        const uint32_t kr = (uint32_t)min(r16, last);
+        uint32_t vr[KPL];
 #pragma unroll
-        for (int e = 0; e < KPL; e++) vrow[e] = r0 + min(vg * KPL + e, last);
-    } else {
-        krow = rm.row(j * 16 + r16);
+        for (int e = 0; e < KPL; e++) vr[e] = (uint32_t)min(vg * KPL + e, last);
+        if (!INT8) {
+            const uint16_t *kb = p.kp + r0 * D, *vb = p.vp + r0 * D;
 #pragma unroll
-        for (int e = 0; e < KPL; e++) vrow[e] = rm.row(j * 16 + vg * KPL + e);
+            for (int i = 0; i < NKB; i++)
+                t.k[i] = *reinterpret_cast<const u32x4 *>(kb + (kr * D + i * 32 + kg * 8));
+#pragma unroll
+            for (int e = 0; e < KPL; e++)
+                t.v[e] = *reinterpret_cast<const u32x4 *>(vb + (vr[e] * D + vc * 8));
+        } else {
+            const int8_t *kb = p.lq + r0 * D, *vb = p.lq + half_q + r0 * D;
+#pragma unroll
+            for (int i = 0; i < NKB; i++) {
+                const uint2 r = *reinterpret_cast<const uint2 *>(kb + (kr * D + i * 32 + kg * 8));
+                t.k[i] = (u32x4){r.x, r.y, 0u, 0u};
+            }
+#pragma unroll
+            for (int e = 0; e < KPL; e++) {
+                const uint2 r = *reinterpret_cast<const uint2 *>(vb + (vr[e] * D + vc * 8));
+                t.v[e] = (u32x4){r.x, r.y, 0u, 0u};
+            }
+            const float *sb = p.ls + r0;
+            t.sk = sb[kr];
+            t.sv = sb[half_s + kr];
+        }
+        return;
     }
+    long long krow, vrow[KPL];
+    krow = rm.row(j * 16 + r16);
+#pragma unroll
+    for (int e = 0; e < KPL; e++) vrow[e] = rm.row(j * 16 + vg * KPL + e);
     if (!INT8) {
 #pragma unroll
         for (int i = 0; i < NKB; i++)
@@ -222,31 +249,37 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
 
     auto compute = [&](const TileRegs<D, INT8> &t, int j) {
         // ---- V rows -> transposed LDS tile vt[d][key] ----
-        {
-            uint32_t words[KPL][4];
-#pragma unroll
-            for (int e = 0; e < KPL; e++) {
-                if (!INT8) {
-#pragma unroll
-                    for (int q2 = 0; q2 < 4; q2++) words[e][q2] = t.v[e][q2];
-                } else {
-                    i8x4_to_bf16(t.v[e][0], words[e][0], words[e][1]);
-                    i8x4_to_bf16(t.v[e][1], words[e][2], words[e][3]);
-                }
-            }
+        if (!INT8) {
             lds_fence();   // the previous tile's reads of myvt are done before overwriting
 #pragma unroll
             for (int dd = 0; dd < 8; dd++) {
-                const int sh = (dd & 1) * 16;
+                const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
                 uint16_t *dst = myvt + (vc * 8 + dd) * VT_ROW + vg * KPL;
                 if (KPL == 4) {
-                    const uint32_t w0 = __builtin_amdgcn_perm(words[1][dd / 2], words[0][dd / 2], sh ? 0x07060302u : 0x05040100u);
-                    const uint32_t w1 = __builtin_amdgcn_perm(words[3][dd / 2], words[2][dd / 2], sh ? 0x07060302u : 0x05040100u);
+                    const uint32_t w0 = __builtin_amdgcn_perm(t.v[1][dd / 2], t.v[0][dd / 2], sel);
+                    const uint32_t w1 = __builtin_amdgcn_perm(t.v[3][dd / 2], t.v[2][dd / 2], sel);
                     *reinterpret_cast<u32x2 *>(dst) = (u32x2){w0, w1};
                 } else {
-                    *reinterpret_cast<uint32_t *>(dst) =
-                        __builtin_amdgcn_perm(words[1][dd / 2], words[0][dd / 2], sh ? 0x07060302u : 0x05040100u);
+                    *reinterpret_cast<uint32_t *>(dst) = __builtin_amdgcn_perm(t.v[1][dd / 2], t.v[0][dd / 2], sel);
                 }
+            }
+        } else {
+            // INT8: convert each byte once and pack two keys' values of one element per
+            // word, which is already the transposed layout (no byte shuffling).
+            float f[KPL][8];
+#pragma unroll
+            for (int e = 0; e < KPL; e++)
+#pragma unroll
+                for (int b8 = 0; b8 < 8; b8++)
+                    f[e][b8] = (float)(int8_t)(t.v[e][b8 >> 2] >> (8 * (b8 & 3)));
+            lds_fence();
+#pragma unroll
+            for (int dd = 0; dd < 8; dd++) {
+                uint16_t *dst = myvt + (vc * 8 + dd) * VT_ROW + vg * KPL;
+                if (KPL == 4)
+                    *reinterpret_cast<u32x2 *>(dst) = (u32x2){pack_bf16x2(f[0][dd], f[1][dd]), pack_bf16x2(f[2][dd], f[3][dd])};
+                else
+                    *reinterpret_cast<uint32_t *>(dst) = pack_bf16x2(f[0][dd], f[1][dd]);
             }
         }
         // ---- S^T = K Q^T ----
@@ -342,21 +375,35 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
         }
     };
 
-    // Two register sets, ping-ponged: tile j + NW is loading while tile j computes. The
-    // prefetch is issued unconditionally (past the last tile it re-reads that tile, unused)
-    // so the count of loads in flight is static and each wait covers only the tile in use.
-    TileRegs<D, INT8> ta, tb;
-    int j = j0 + w;
+    // Two register sets, ping-ponged: the next group of TPI tiles is loading while the
+    // current one computes. INT8 tiles are half the bytes, so INT8 waves take two tiles
+    // per step to keep as many bytes in flight as bf16 waves. The prefetch is issued
+    // unconditionally (past the last tile it re-reads that tile, unused) so the count of
+    // loads in flight is static and each wait covers only the tiles in use.
+    constexpr int TPI = INT8 ? 2 : 1;
+    constexpr int STRIDE = NW * TPI;
+    TileRegs<D, INT8> ta[TPI], tb[TPI];
+    auto ld = [&](TileRegs<D, INT8> (&t)[TPI], int jj) {
+#pragma unroll
+        for (int e = 0; e < TPI; e++)
+            load_tile<D, INT8, PG16>(t[e], p, rm, min(jj + e, j1 - 1), r16, kg, vg, vc, half_q, half_s);
+    };
+    auto run = [&](const TileRegs<D, INT8> (&t)[TPI], int jj) {
+#pragma unroll
+        for (int e = 0; e < TPI; e++)
+            if (jj + e < j1) compute(t[e], jj + e);
+    };
+    int j = j0 + TPI * w;
     if (j < j1) {
-        load_tile<D, INT8, PG16>(ta, p, rm, j, r16, kg, vg, vc, half_q, half_s);
+        ld(ta, j);
         while (true) {
-            load_tile<D, INT8, PG16>(tb, p, rm, min(j + NW, j1 - 1), r16, kg, vg, vc, half_q, half_s);
-            compute(ta, j);
-            j += NW;
+            ld(tb, j + STRIDE);
+            run(ta, j);
+            j += STRIDE;
             if (j >= j1) break;
-            load_tile<D, INT8, PG16>(ta, p, rm, min(j + NW, j1 - 1), r16, kg, vg, vc, half_q, half_s);
-            compute(tb, j);
-            j += NW;
+            ld(ta, j + STRIDE);
+            run(tb, j);
+            j += STRIDE;
             if (j >= j1) break;
         }
     }
