@@ -25,17 +25,20 @@ FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",
     # Packed FP32 (v_pk_*_f32) is off for every kernel: hipcc would otherwise form it.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in VGPRs (not AGPRs): avoids per-tile AGPR<->VGPR copies around
-    # the online-softmax rescale.
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-I", os.path.join(ROOT, "include"), "-I", CSRC,
     "-Wall", "-Wno-unused-function",
 ]
 
 
+# MFMA accumulators in VGPRs (not AGPRs) avoid AGPR<->VGPR copies around the softmax
+# rescale; the wide decode variants need the AGPRs for their large accumulators.
+AGPR_FILES = {"pa_decode_wide.hip"}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    extra = [] if os.path.basename(src) in AGPR_FILES else ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+    cmd = [HIPCC, *FLAGS, *extra, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

@@ -1,468 +1,11 @@
-// Split-KV paged decode / verify attention on bf16 MFMA (gfx950), dense bf16 or INT8 cache.
-//
-// Reference: attention_decode_kernel / decode_body / attention_combine_kernel
-// (src/ops/tile/attention.jl:185-245) and its INT8 variant (:68-95, :194-202).
-//
-// Work decomposition. The G = Hq/Hk query heads that share a KV head, times the n query
-// tokens of the step, are packed into M = G*n query rows (row r = g + G t, as the
-// reference's packed tile). One work-group (4 waves) handles one (sequence, KV head,
-// split); a split is a contiguous range of 16-key tiles of the sequence, and the waves of
-// the group take every 4th tile of it, each with its own online-softmax state. The grid
-// depends only on host shapes (B, Hk, splits), never on the context length, so a captured
-// graph stays valid as sequences grow; splits that get no keys write a neutral partial.
-//
-// Per 16-key tile and wave (lane l; r = l % 16 is the query row within a 16-row block,
-// k = l / 16 its key/element group):
-//   S^T = K Q^T      v_mfma_f32_16x16x32_bf16, A = K rows loaded straight from HBM
-//                    (lane: key l%16, 8 head-dim elements per 32-wide block, 16 B loads);
-//                    C lands as lane (row r, keys 4k..4k+3).
-//   online softmax   exp2 domain (scale * log2 e), per lane for its own row; the row max
-//                    over the tile's 16 keys is two xor shuffles (lanes r, r+16, r+32, r+48).
-//   O^T += V^T P^T   v_mfma_f32_16x16x16_bf16, B = P^T comes straight from the S^T
-//                    registers (same lane layout), A = V^T read from a per-wave LDS tile
-//                    that holds V transposed (written from coalesced 16 B row loads).
-//                    O^T's lane layout keeps each lane on its own row, so the rescale by
-//                    alpha needs no shuffles.
-// INT8 keys and values are exact in bf16; a key's scale multiplies its scores and a
-// value's scale its probability (src/ops/quant.jl:56-72); queries are multiplied by the
-// keys' smoothing and rounded to bf16 (attention.jl:90-95).
-//
-// At the end the four waves merge their (m, l, O) through LDS and the group writes one
-// Float32 partial (acc[D], m, l) per packed row; the combine kernel merges the splits:
-// w_s = exp2(m_s - max m), o = sum acc_s w_s / sum l_s w_s.
 #include <stdlib.h>
 
-#include "common.hpp"
+#include "pa_decode.hpp"
 
 using namespace ti;
+using namespace ti_decode;
 
 namespace {
-
-struct DecodeParams {
-    const uint16_t *q;
-    uint16_t *out;
-    const uint16_t *kp, *vp;
-    const int8_t *lq;
-    const float *ls, *smooth;
-    const int32_t *positions, *qsl, *bt;
-    float *part;
-    int bt_stride, num_pages, P, pshift, Hk, Hq, G, nmax, M, splits, causal;
-    float scale_log2;
-};
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-// Transposed V tile in LDS: [D][16 keys] bf16, rows padded to 40 B (conflict-free reads).
-constexpr int VT_ROW = 20;  // uint16 per padded row
-constexpr float RESCALE_LOG2 = 8.0f;
-
-__device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-// 8 int8 -> 8 bf16 words (exact).
-__device__ __forceinline__ u32x4 i8x8_to_bf16(uint2 v) {
-    u32x4 r;
-    uint32_t a, b, c, d;
-    i8x4_to_bf16(v.x, a, b);
-    i8x4_to_bf16(v.y, c, d);
-    r[0] = a; r[1] = b; r[2] = c; r[3] = d;
-    return r;
-}
-
-// One 16-key tile's raw loads, held in registers from issue to use (software pipeline).
-template <int D, bool INT8>
-struct TileRegs {
-    static constexpr int NKB = D / 32;
-    static constexpr int KPL = 16 * (D / 8) / 64;
-    u32x4 k[NKB];          // dense: 8 bf16 per 32-wide block;   INT8: .xy = 8 int8
-    u32x4 v[KPL];          // dense: 8 bf16 of key vg*KPL + e;   INT8: .xy = 8 int8
-    float sk, sv;          // INT8 scales of this lane's K key
-};
-
-// Pool row of key position pos of KV head h. PG16: the 16-key tile lies in one page
-// (P % 16 == 0), so the caller passes the page's first row; otherwise a per-key lookup
-// with the position clamped into the sequence (rows past len are never used unmasked).
-struct RowMap {
-    const int32_t *bt;
-    int P, pshift, Hk, h, num_pages, len;
-    __device__ __forceinline__ int page_index(int pos) const {
-        return pshift >= 0 ? (pos >> pshift) : pos / P;
-    }
-    __device__ __forceinline__ int page_offset(int pos) const {
-        return pshift >= 0 ? (pos & (P - 1)) : pos % P;
-    }
-    __device__ __forceinline__ long long row(int pos) const {
-        pos = min(pos, len - 1);
-        const int pg = page_of(bt, page_index(pos), num_pages);
-        return ((long long)pg * Hk + h) * P + page_offset(pos);
-    }
-    // pos wave-uniform: scalar block-table load
-    __device__ __forceinline__ long long row_s(int pos) const {
-        pos = min(pos, len - 1);
-        const int pg = page_of_s(bt, page_index(pos), num_pages);
-        return ((long long)pg * Hk + h) * P + page_offset(pos);
-    }
-};
-
-template <int D, bool INT8, bool PG16>
-__device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodeParams &p,
-                                          const RowMap &rm, int j, int r16, int kg, int vg,
-                                          int vc, size_t half_q, size_t half_s) {
-    constexpr int NKB = TileRegs<D, INT8>::NKB, KPL = TileRegs<D, INT8>::KPL;
-    if (PG16) {
-        // One page per tile: a wave-uniform 64-bit base plus small per-lane 32-bit offsets
-        // (scalar-base addressing, no 64-bit vector math). Keys past len read the last
-        // valid key's row, whose finite values meet p = 0 (never stale memory that could
-        // hold NaN).
-        const long long r0 = rm.row_s(j * 16);
-        const int last = rm.len - 1 - j * 16;
-        const uint32_t kr = (uint32_t)min(r16, last);
-        uint32_t vr[KPL];
-#pragma unroll
-        for (int e = 0; e < KPL; e++) vr[e] = (uint32_t)min(vg * KPL + e, last);
-        if (!INT8) {
-            const uint16_t *kb = p.kp + r0 * D, *vb = p.vp + r0 * D;
-#pragma unroll
-            for (int i = 0; i < NKB; i++)
-                t.k[i] = *reinterpret_cast<const u32x4 *>(kb + (kr * D + i * 32 + kg * 8));
-#pragma unroll
-            for (int e = 0; e < KPL; e++)
-                t.v[e] = *reinterpret_cast<const u32x4 *>(vb + (vr[e] * D + vc * 8));
-        } else {
-            const int8_t *kb = p.lq + r0 * D, *vb = p.lq + half_q + r0 * D;
-#pragma unroll
-            for (int i = 0; i < NKB; i++) {
-                const uint2 r = *reinterpret_cast<const uint2 *>(kb + (kr * D + i * 32 + kg * 8));
-                t.k[i] = (u32x4){r.x, r.y, 0u, 0u};
-            }
-#pragma unroll
-            for (int e = 0; e < KPL; e++) {
-                const uint2 r = *reinterpret_cast<const uint2 *>(vb + (vr[e] * D + vc * 8));
-                t.v[e] = (u32x4){r.x, r.y, 0u, 0u};
-            }
-            const float *sb = p.ls + r0;
-            t.sk = sb[kr];
-            t.sv = sb[half_s + kr];
-        }
-        return;
-    }
-    long long krow, vrow[KPL];
-    krow = rm.row(j * 16 + r16);
-#pragma unroll
-    for (int e = 0; e < KPL; e++) vrow[e] = rm.row(j * 16 + vg * KPL + e);
-    if (!INT8) {
-#pragma unroll
-        for (int i = 0; i < NKB; i++)
-            t.k[i] = *reinterpret_cast<const u32x4 *>(p.kp + krow * D + i * 32 + kg * 8);
-#pragma unroll
-        for (int e = 0; e < KPL; e++)
-            t.v[e] = *reinterpret_cast<const u32x4 *>(p.vp + vrow[e] * D + vc * 8);
-    } else {
-#pragma unroll
-        for (int i = 0; i < NKB; i++) {
-            const uint2 r = *reinterpret_cast<const uint2 *>(p.lq + krow * D + i * 32 + kg * 8);
-            t.k[i] = (u32x4){r.x, r.y, 0u, 0u};
-        }
-#pragma unroll
-        for (int e = 0; e < KPL; e++) {
-            const uint2 r = *reinterpret_cast<const uint2 *>(p.lq + half_q + vrow[e] * D + vc * 8);
-            t.v[e] = (u32x4){r.x, r.y, 0u, 0u};
-        }
-        t.sk = p.ls[krow];
-        t.sv = p.ls[half_s + krow];
-    }
-}
-
-template <int D, int ROWB, bool INT8, bool PG16, int NW>
-__global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
-    constexpr int NKB = D / 32;          // 32-wide head-dim blocks (QK MFMAs per tile)
-    constexpr int NDT = D / 16;          // 16-wide head-dim tiles (PV MFMAs per tile)
-    constexpr int CPR = D / 8;           // 8-element chunks per V row
-    constexpr int KPL = 16 * CPR / 64;   // keys per lane in the V load (4 for D=128)
-    constexpr int MP = ROWB * 16;        // padded rows
-
-    // Per-wave transposed V tiles during the key loop; afterwards the same LDS holds each
-    // wave's (O, m, l) slab for the merge (rows of D + 4 floats, 16-B aligned).
-    constexpr int MROW = D + 4;
-    constexpr int VT_BYTES = NW * D * VT_ROW * 2;
-    constexpr int SLAB_BYTES = NW * MP * MROW * 4;
-    __shared__ __attribute__((aligned(16))) char smem_raw[VT_BYTES > SLAB_BYTES ? VT_BYTES : SLAB_BYTES];
-    uint16_t (*vt)[D * VT_ROW] = reinterpret_cast<uint16_t (*)[D * VT_ROW]>(smem_raw);
-    float *mslab = reinterpret_cast<float *>(smem_raw);
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
-    const int r16 = lane & 15, kg = lane >> 4;
-    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
-    if (nb <= 0) return;
-    const int start = p.positions[tok0], len = start + nb;
-    const int ntiles = (len + 15) >> 4;
-    const int per = (ntiles + p.splits - 1) / p.splits;
-    const int j0 = s * per, j1 = min(j0 + per, ntiles);
-    const size_t half_q = (size_t)p.num_pages * p.Hk * p.P * D;
-    const size_t half_s = (size_t)p.num_pages * p.Hk * p.P;
-    const RowMap rm{p.bt + (size_t)b * p.bt_stride, p.P, p.pshift, p.Hk, h, p.num_pages, len};
-    // Keys up to mask_from are visible to every row; later tiles need the mask.
-    const int mask_from = p.causal ? start : len - 1;
-
-    // Query operands (B of S^T = K Q^T): row rb*16 + r16, elements i*32 + kg*8 .. +8.
-    bf16x8 qreg[ROWB][NKB];
-    int qpos[ROWB];
-#pragma unroll
-    for (int rb = 0; rb < ROWB; rb++) {
-        const int r = rb * 16 + r16, t = r / p.G, g = r - t * p.G;
-        const bool ok = r < p.M && t < nb;
-        qpos[rb] = p.causal && ok ? start + t : len - 1;
-        const uint16_t *qr = p.q + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
-#pragma unroll
-        for (int i = 0; i < NKB; i++) {
-            const int d0 = i * 32 + kg * 8;
-            if (!ok) {
-                qreg[rb][i] = as_bf16x8((u32x4){0u, 0u, 0u, 0u});
-            } else if (!INT8) {
-                qreg[rb][i] = as_bf16x8(*reinterpret_cast<const u32x4 *>(qr + d0));
-            } else {
-                const u32x4 raw = *reinterpret_cast<const u32x4 *>(qr + d0);
-                u32x4 wv;
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    wv[e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * p.smooth[d0 + 2 * e],
-                                        __uint_as_float(raw[e] & 0xffff0000u) * p.smooth[d0 + 2 * e + 1]);
-                qreg[rb][i] = as_bf16x8(wv);
-            }
-        }
-    }
-
-    f32x4 o[ROWB][NDT];
-    float m[ROWB], l[ROWB];
-#pragma unroll
-    for (int rb = 0; rb < ROWB; rb++) {
-        m[rb] = NEG_BIG;
-        l[rb] = 0.0f;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) o[rb][dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    }
-
-    uint16_t *myvt = vt[w];
-    const int vc = lane % CPR, vg = lane / CPR;   // V load: chunk, key group
-
-    auto compute = [&](const TileRegs<D, INT8> &t, int j) {
-        // ---- V rows -> transposed LDS tile vt[d][key] ----
-        if (!INT8) {
-            lds_fence();   // the previous tile's reads of myvt are done before overwriting
-#pragma unroll
-            for (int dd = 0; dd < 8; dd++) {
-                const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-                uint16_t *dst = myvt + (vc * 8 + dd) * VT_ROW + vg * KPL;
-                if (KPL == 4) {
-                    const uint32_t w0 = __builtin_amdgcn_perm(t.v[1][dd / 2], t.v[0][dd / 2], sel);
-                    const uint32_t w1 = __builtin_amdgcn_perm(t.v[3][dd / 2], t.v[2][dd / 2], sel);
-                    *reinterpret_cast<u32x2 *>(dst) = (u32x2){w0, w1};
-                } else {
-                    *reinterpret_cast<uint32_t *>(dst) = __builtin_amdgcn_perm(t.v[1][dd / 2], t.v[0][dd / 2], sel);
-                }
-            }
-        } else {
-            // INT8: convert each byte once and pack two keys' values of one element per
-            // word, which is already the transposed layout (no byte shuffling).
-            float f[KPL][8];
-#pragma unroll
-            for (int e = 0; e < KPL; e++)
-#pragma unroll
-                for (int b8 = 0; b8 < 8; b8++)
-                    f[e][b8] = (float)(int8_t)(t.v[e][b8 >> 2] >> (8 * (b8 & 3)));
-            lds_fence();
-#pragma unroll
-            for (int dd = 0; dd < 8; dd++) {
-                uint16_t *dst = myvt + (vc * 8 + dd) * VT_ROW + vg * KPL;
-                if (KPL == 4)
-                    *reinterpret_cast<u32x2 *>(dst) = (u32x2){pack_bf16x2(f[0][dd], f[1][dd]), pack_bf16x2(f[2][dd], f[3][dd])};
-                else
-                    *reinterpret_cast<uint32_t *>(dst) = pack_bf16x2(f[0][dd], f[1][dd]);
-            }
-        }
-        // ---- S^T = K Q^T ----
-        bf16x8 kreg[NKB];
-#pragma unroll
-        for (int i = 0; i < NKB; i++) {
-            if (!INT8) {
-                kreg[i] = as_bf16x8(t.k[i]);
-            } else {
-                u32x4 wv;
-                uint32_t a0, a1, a2, a3;
-                i8x4_to_bf16(t.k[i][0], a0, a1);
-                i8x4_to_bf16(t.k[i][1], a2, a3);
-                wv[0] = a0; wv[1] = a1; wv[2] = a2; wv[3] = a3;
-                kreg[i] = as_bf16x8(wv);
-            }
-        }
-        f32x4 sc[ROWB];
-#pragma unroll
-        for (int rb = 0; rb < ROWB; rb++) {
-            sc[rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < NKB; i++)
-                sc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kreg[i], qreg[rb][i], sc[rb], 0, 0, 0);
-        }
-        // Scales of this lane's 4 score keys (kg*4 + e), from the lanes that loaded them.
-        float skk[4], svk[4];
-        if (INT8) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                skk[e] = __shfl(t.sk, kg * 4 + e);
-                svk[e] = __shfl(t.sv, kg * 4 + e);
-            }
-        }
-        // ---- online softmax + P^T operands ----
-        // Lazy rescaling: m is a reference max that only moves when a tile's max exceeds
-        // it by more than RESCALE_LOG2 (then p <= 2^RESCALE_LOG2, safe in bf16 and fp32);
-        // l and O always use the same reference, so the result is exact.
-        const bool need_mask = j * 16 + 15 > mask_from;
-        s16x4 pop[ROWB];
-        float x[ROWB][4], mt[ROWB];
-        bool grow = false;
-#pragma unroll
-        for (int rb = 0; rb < ROWB; rb++) {
-            mt[rb] = -INFINITY;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float v = sc[rb][e];
-                if (INT8) v *= skk[e];
-                v *= p.scale_log2;
-                if (need_mask) {
-                    const int kp = j * 16 + kg * 4 + e;
-                    v = (kp <= qpos[rb] && kp < len) ? v : -INFINITY;
-                }
-                x[rb][e] = v;
-                mt[rb] = fmaxf(mt[rb], v);
-            }
-            grow |= mt[rb] > m[rb] + RESCALE_LOG2;
-        }
-        if (__any(grow)) {
-#pragma unroll
-            for (int rb = 0; rb < ROWB; rb++) {
-                float t2 = fmaxf(mt[rb], __shfl_xor(mt[rb], 16));
-                t2 = fmaxf(t2, __shfl_xor(t2, 32));
-                const float mn = fmaxf(m[rb], t2);
-                const float alpha = fast_exp2(m[rb] - mn);
-                m[rb] = mn;
-                l[rb] *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < NDT; dt++) o[rb][dt] *= alpha;
-            }
-        }
-#pragma unroll
-        for (int rb = 0; rb < ROWB; rb++) {
-            float ps = 0.0f, pe[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                pe[e] = fast_exp2(x[rb][e] - m[rb]);
-                ps += pe[e];
-                if (INT8) pe[e] *= svk[e];
-            }
-            l[rb] += ps;
-            pop[rb] = __builtin_bit_cast(s16x4, (u32x2){pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3])});
-        }
-        // ---- O^T += V^T P^T ----
-        lds_fence();   // this tile's V^T is in LDS
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++) {
-            const s16x4 a = __builtin_bit_cast(s16x4, *reinterpret_cast<const u32x2 *>(myvt + (dt * 16 + r16) * VT_ROW + kg * 4));
-#pragma unroll
-            for (int rb = 0; rb < ROWB; rb++)
-                o[rb][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop[rb], o[rb][dt], 0, 0, 0);
-        }
-    };
-
-    // Two register sets, ping-ponged: the next group of TPI tiles is loading while the
-    // current one computes. INT8 tiles are half the bytes, so INT8 waves take two tiles
-    // per step to keep as many bytes in flight as bf16 waves. The prefetch is issued
-    // unconditionally (past the last tile it re-reads that tile, unused) so the count of
-    // loads in flight is static and each wait covers only the tiles in use.
-    constexpr int TPI = INT8 ? 2 : 1;
-    constexpr int STRIDE = NW * TPI;
-    TileRegs<D, INT8> ta[TPI], tb[TPI];
-    auto ld = [&](TileRegs<D, INT8> (&t)[TPI], int jj) {
-#pragma unroll
-        for (int e = 0; e < TPI; e++)
-            load_tile<D, INT8, PG16>(t[e], p, rm, min(jj + e, j1 - 1), r16, kg, vg, vc, half_q, half_s);
-    };
-    auto run = [&](const TileRegs<D, INT8> (&t)[TPI], int jj) {
-#pragma unroll
-        for (int e = 0; e < TPI; e++)
-            if (jj + e < j1) compute(t[e], jj + e);
-    };
-    int j = j0 + TPI * w;
-    if (j < j1) {
-        ld(ta, j);
-        while (true) {
-            ld(tb, j + STRIDE);
-            run(ta, j);
-            j += STRIDE;
-            if (j >= j1) break;
-            ld(ta, j + STRIDE);
-            run(tb, j);
-            j += STRIDE;
-            if (j >= j1) break;
-        }
-    }
-
-    // ---- merge the waves' states (same rows, disjoint keys) through LDS slabs ----
-#pragma unroll
-    for (int rb = 0; rb < ROWB; rb++) {
-        l[rb] += __shfl_xor(l[rb], 16);
-        l[rb] += __shfl_xor(l[rb], 32);
-    }
-    __syncthreads();   // every wave is done with its V tile
-#pragma unroll
-    for (int rb = 0; rb < ROWB; rb++) {
-        float *my = mslab + ((size_t)w * MP + rb * 16 + r16) * MROW;
-#pragma unroll
-        for (int dt = 0; dt < NDT; dt++)
-            *reinterpret_cast<f32x4 *>(my + dt * 16 + kg * 4) = o[rb][dt];
-        if (kg == 0) {
-            my[D] = m[rb];
-            my[D + 1] = l[rb];
-        }
-    }
-    __syncthreads();
-    const size_t unit = ((size_t)b * p.Hk + h) * p.splits + s;
-    for (int item = threadIdx.x; item < p.M * (D / 4); item += NW * 64) {
-        const int r = item / (D / 4), d4 = (item % (D / 4)) * 4;
-        float mx = NEG_BIG;
-#pragma unroll
-        for (int wi = 0; wi < NW; wi++) mx = fmaxf(mx, mslab[((size_t)wi * MP + r) * MROW + D]);
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        float lsum = 0.0f;
-#pragma unroll
-        for (int wi = 0; wi < NW; wi++) {
-            const float *src = mslab + ((size_t)wi * MP + r) * MROW;
-            const float wgt = fast_exp2(src[D] - mx);
-            lsum += src[D + 1] * wgt;
-            acc += *reinterpret_cast<const f32x4 *>(src + d4) * wgt;
-        }
-        if (p.splits == 1) {
-            // One split: this group saw every key; normalize and write the output rows.
-            const int t = r / p.G, g = r - t * p.G;
-            if (t < nb) {
-                const float inv = 1.0f / lsum;
-                uint16_t *o16 = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D + d4;
-                *reinterpret_cast<u32x2 *>(o16) = (u32x2){pack_bf16x2(acc[0] * inv, acc[1] * inv),
-                                                          pack_bf16x2(acc[2] * inv, acc[3] * inv)};
-            }
-        } else {
-            // The split's partial: part[unit][r][D + 2] = (acc, m, l).
-            float *dst = p.part + (unit * (size_t)p.M + r) * (D + 2);
-#pragma unroll
-            for (int e = 0; e < 4; e++) dst[d4 + e] = acc[e];
-            if (d4 == 0) {
-                dst[D] = mx;
-                dst[D + 1] = lsum;
-            }
-        }
-    }
-}
 
 // Merge the splits of one packed row: grid (M, Hk, B), 256 threads. The four waves take
 // every 4th split; lane owns head-dim elements lane + 64 k. Partials then meet in LDS.
@@ -531,12 +74,12 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
 
 template <int D, bool INT8, bool PG16, int NW>
 void launch_decode_d(const DecodeParams &p, int rowb, dim3 grid, hipStream_t s) {
-    // 8-wave groups only for up to 32 packed rows (their merge slabs must fit the LDS).
+    // 8-wave groups only for up to 32 packed rows (their merge slabs must fit the LDS);
+    // 48 and 64 rows run the variants built in pa_decode_wide.hip.
     switch (rowb) {
         case 1: decode_kernel<D, 1, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
         case 2: decode_kernel<D, 2, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
-        case 3: decode_kernel<D, 3, INT8, PG16, 4><<<grid, 4 * 64, 0, s>>>(p); break;
-        default: decode_kernel<D, 4, INT8, PG16, 4><<<grid, 4 * 64, 0, s>>>(p); break;
+        default: ti_launch_decode_wide(p, D, rowb, INT8, PG16, grid, s); break;
     }
 }
 
