@@ -7,69 +7,40 @@ using namespace ti_decode;
 
 namespace {
 
-// Merge the splits of one packed row: grid (M, Hk, B), 256 threads. The four waves take
-// every 4th split; lane owns head-dim elements lane + 64 k. Partials then meet in LDS.
+// Merge the splits of packed rows: grid (ceil(M / 4), Hk, B), four waves, one row per
+// wave; lane owns head-dim elements lane + 64 k. The running maxima and sums are
+// wave-uniform loads; the partial rows are read coalesced, with no LDS and no barrier.
 template <int D>
 __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     constexpr int PER = D / 64;
-    const int r = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = blockIdx.y, b = blockIdx.z;
+    if (r >= p.M) return;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
     const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
     const int t = r / p.G, g = r - t * p.G;
     if (t >= nb) return;
     const size_t stride = (size_t)p.M * (D + 2);
     const float *base = p.part + ((size_t)b * p.Hk + h) * p.splits * stride + (size_t)r * (D + 2);
-    __shared__ float ws[256];
-    __shared__ float red[4];
-    __shared__ float accs[4][D];
-    // global max of the splits' running maxima
     float mx = NEG_BIG;
-    for (int sp = tid; sp < p.splits; sp += 256) mx = fmaxf(mx, base[sp * stride + D]);
-    mx = wave_max(mx);
-    if (lane == 0) red[w] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    float ls = 0.0f;
-    for (int sp = tid; sp < p.splits; sp += 256) {
-        const float wgt = fast_exp2(base[sp * stride + D] - mx);
-        ws[sp] = wgt;
-        ls += base[sp * stride + D + 1] * wgt;
+#pragma unroll 8
+    for (int sp = 0; sp < p.splits; sp++) mx = fmaxf(mx, base[sp * stride + D]);
+    float acc[PER], lsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) acc[k] = 0.0f;
+#pragma unroll 8
+    for (int sp = 0; sp < p.splits; sp++) {
+        const float *src = base + sp * stride;
+        const float wgt = fast_exp2(src[D] - mx);
+        lsum += src[D + 1] * wgt;
+#pragma unroll
+        for (int k = 0; k < PER; k++) acc[k] += src[lane + 64 * k] * wgt;
     }
-    ls = wave_sum(ls);
-    if (lane == 0) red[w] = ls;
-    __syncthreads();
-    ls = red[0] + red[1] + red[2] + red[3];
-    float acc[PER], acc2[PER];
+    const float inv = 1.0f / lsum;
+    uint16_t *o = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
 #pragma unroll
-    for (int k = 0; k < PER; k++) acc[k] = acc2[k] = 0.0f;
-    int sp = w;
-    for (; sp + 4 < p.splits; sp += 8) {
-        const float w0 = ws[sp], w1 = ws[sp + 4];
-#pragma unroll
-        for (int k = 0; k < PER; k++) {
-            acc[k] += base[sp * stride + lane + 64 * k] * w0;
-            acc2[k] += base[(sp + 4) * stride + lane + 64 * k] * w1;
-        }
-    }
-    if (sp < p.splits) {
-        const float w0 = ws[sp];
-#pragma unroll
-        for (int k = 0; k < PER; k++) acc[k] += base[sp * stride + lane + 64 * k] * w0;
-    }
-#pragma unroll
-    for (int k = 0; k < PER; k++) accs[w][lane + 64 * k] = acc[k] + acc2[k];
-    __syncthreads();
-    if (w == 0) {
-        uint16_t *o = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
-        const float inv = 1.0f / ls;
-#pragma unroll
-        for (int k = 0; k < PER; k++) {
-            const int d = lane + 64 * k;
-            o[d] = f2bf((accs[0][d] + accs[1][d] + accs[2][d] + accs[3][d]) * inv);
-        }
-    }
+    for (int k = 0; k < PER; k++) o[lane + 64 * k] = f2bf(acc[k] * inv);
 }
 
 template <int D, bool INT8, bool PG16, int NW>
@@ -176,7 +147,7 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
     }
     if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
     if (pl.splits == 1) return TI_OK;
-    dim3 cgrid(pl.rows, c->kv_heads, a->num_seqs);
+    dim3 cgrid((pl.rows + 3) / 4, c->kv_heads, a->num_seqs);
     if (c->head_dim == 128) combine_kernel<128><<<cgrid, 256, 0, s>>>(p);
     else combine_kernel<64><<<cgrid, 256, 0, s>>>(p);
     return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
