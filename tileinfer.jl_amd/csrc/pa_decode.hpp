@@ -19,8 +19,9 @@
 //   online softmax   exp2 domain (scale * log2 e), per lane for its own row; the row max
 //                    over the tile's 16 keys is two xor shuffles (lanes r, r+16, r+32, r+48).
 //   O^T += V^T P^T   v_mfma_f32_16x16x16_bf16, B = P^T comes straight from the S^T
-//                    registers (same lane layout), A = V^T read from a per-wave LDS tile
-//                    that holds V transposed (written from coalesced 16 B row loads).
+//                    registers (same lane layout), A = V^T built by ds_read_b64_tr_b16
+//                    from a per-wave row-major V tile in LDS (written with 16-B stores
+//                    straight from the coalesced row loads).
 //                    O^T's lane layout keeps each lane on its own row, so the rescale by
 //                    alpha needs no shuffles.
 // INT8 keys and values are exact in bf16; a key's scale multiplies its scores and a
@@ -38,6 +39,8 @@ using namespace ti;
 
 namespace ti_decode {
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
 struct DecodeParams {
     const uint16_t *q;
     uint16_t *out;
@@ -50,13 +53,21 @@ struct DecodeParams {
     float scale_log2;
 };
 
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-// Transposed V tile in LDS: [D][16 keys] bf16, rows padded to 40 B (conflict-free reads).
-constexpr int VT_ROW = 20;  // uint16 per padded row
+// Per-wave V tile in LDS: [16 keys][D + 16] bf16, row-major. The row stride (an odd
+// multiple of 32 B) puts the 8 rows x 32 B that 32 lanes of a transposing read touch on
+// 64 distinct banks; 16 lanes storing one key's row write 256 contiguous bytes.
+template <int D>
+constexpr int vtile_row() { return D + 16; }
 constexpr float RESCALE_LOG2 = 8.0f;
 
 __device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element (j % 4) of the
+// 4 bf16 that lanes j/4, j/4 + 4, j/4 + 8 and j/4 + 12 address.
+__device__ __forceinline__ s16x4 lds_tr16(const uint16_t *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4 *)(__attribute__((address_space(3))) uint16_t *)p);
+}
 
 // 8 int8 -> 8 bf16 words (exact).
 __device__ __forceinline__ u32x4 i8x8_to_bf16(uint2 v) {
@@ -183,10 +194,11 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     // Per-wave transposed V tiles during the key loop; afterwards the same LDS holds each
     // wave's (O, m, l) slab for the merge (rows of D + 4 floats, 16-B aligned).
     constexpr int MROW = D + 4;
-    constexpr int VT_BYTES = NW * D * VT_ROW * 2;
+    constexpr int VROW = vtile_row<D>();
+    constexpr int VT_BYTES = NW * 16 * VROW * 2;
     constexpr int SLAB_BYTES = NW * MP * MROW * 4;
     __shared__ __attribute__((aligned(16))) char smem_raw[VT_BYTES > SLAB_BYTES ? VT_BYTES : SLAB_BYTES];
-    uint16_t (*vt)[D * VT_ROW] = reinterpret_cast<uint16_t (*)[D * VT_ROW]>(smem_raw);
+    uint16_t (*vt)[16 * VROW] = reinterpret_cast<uint16_t (*)[16 * VROW]>(smem_raw);
     float *mslab = reinterpret_cast<float *>(smem_raw);
 
     const int lane = threadIdx.x & 63;
@@ -248,40 +260,14 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     const int vc = lane % CPR, vg = lane / CPR;   // V load: chunk, key group
 
     auto compute = [&](const TileRegs<D, INT8> &t, int j) {
-        // ---- V rows -> transposed LDS tile vt[d][key] ----
-        if (!INT8) {
-            lds_fence();   // the previous tile's reads of myvt are done before overwriting
+        // ---- V rows -> row-major LDS tile (INT8 converted to bf16, exact) ----
+        u32x4 vrows[KPL];
 #pragma unroll
-            for (int dd = 0; dd < 8; dd++) {
-                const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-                uint16_t *dst = myvt + (vc * 8 + dd) * VT_ROW + vg * KPL;
-                if (KPL == 4) {
-                    const uint32_t w0 = __builtin_amdgcn_perm(t.v[1][dd / 2], t.v[0][dd / 2], sel);
-                    const uint32_t w1 = __builtin_amdgcn_perm(t.v[3][dd / 2], t.v[2][dd / 2], sel);
-                    *reinterpret_cast<u32x2 *>(dst) = (u32x2){w0, w1};
-                } else {
-                    *reinterpret_cast<uint32_t *>(dst) = __builtin_amdgcn_perm(t.v[1][dd / 2], t.v[0][dd / 2], sel);
-                }
-            }
-        } else {
-            // INT8: convert each byte once and pack two keys' values of one element per
-            // word, which is already the transposed layout (no byte shuffling).
-            float f[KPL][8];
+        for (int e = 0; e < KPL; e++) vrows[e] = INT8 ? i8x8_to_bf16(make_uint2(t.v[e][0], t.v[e][1])) : t.v[e];
+        lds_fence();   // the previous tile's reads of myvt are done before overwriting
 #pragma unroll
-            for (int e = 0; e < KPL; e++)
-#pragma unroll
-                for (int b8 = 0; b8 < 8; b8++)
-                    f[e][b8] = (float)(int8_t)(t.v[e][b8 >> 2] >> (8 * (b8 & 3)));
-            lds_fence();
-#pragma unroll
-            for (int dd = 0; dd < 8; dd++) {
-                uint16_t *dst = myvt + (vc * 8 + dd) * VT_ROW + vg * KPL;
-                if (KPL == 4)
-                    *reinterpret_cast<u32x2 *>(dst) = (u32x2){pack_bf16x2(f[0][dd], f[1][dd]), pack_bf16x2(f[2][dd], f[3][dd])};
-                else
-                    *reinterpret_cast<uint32_t *>(dst) = pack_bf16x2(f[0][dd], f[1][dd]);
-            }
-        }
+        for (int e = 0; e < KPL; e++)
+            *reinterpret_cast<u32x4 *>(myvt + (vg * KPL + e) * VROW + vc * 8) = vrows[e];
         // ---- S^T = K Q^T ----
         bf16x8 kreg[NKB];
 #pragma unroll
@@ -368,10 +354,19 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
         lds_fence();   // this tile's V^T is in LDS
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) {
-            const s16x4 a = __builtin_bit_cast(s16x4, *reinterpret_cast<const u32x2 *>(myvt + (dt * 16 + r16) * VT_ROW + kg * 4));
+            const s16x4 a = lds_tr16(myvt + (4 * kg + (r16 >> 2)) * VROW + dt * 16 + 4 * (r16 & 3));
 #pragma unroll
             for (int rb = 0; rb < ROWB; rb++)
                 o[rb][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop[rb], o[rb][dt], 0, 0, 0);
+        }
+        if constexpr (ROWB >= 3) {
+            // The 48/64-row variants accumulate in AGPRs. Pin the accumulators there at
+            // the end of each tile: otherwise the compiler carries a VGPR copy of all of
+            // them around the loop (for the rare rescale) and re-reads it every tile.
+#pragma unroll
+            for (int rb = 0; rb < ROWB; rb++)
+#pragma unroll
+                for (int dt = 0; dt < NDT; dt++) asm volatile("" : "+a"(o[rb][dt]));
         }
     };
 

@@ -51,11 +51,12 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // One key group's LDS: K and V tiles row-major, double-buffered. Row strides (in bf16)
 // D + 8 for K (16-B reads by 16 consecutive lanes of 16 keys hit 64 distinct banks) and
-// D + 16 for V (the transposing reads of 4 rows x 32 B are bank-disjoint).
+// D + 32 for V: a transposing read by 32 lanes covers 4 rows x 64 B, and rows 16 banks
+// apart make those 256 B bank-disjoint.
 template <int D>
 struct Smem {
     static constexpr int KROW = D + 8;
-    static constexpr int VROW = D + 16;
+    static constexpr int VROW = D + 32;
     uint16_t k[2][KT * KROW];
     uint16_t v[2][KT * VROW];
     float sk[2][KT], sv[2][KT];
@@ -429,22 +430,38 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
             my[D + 1] = l;
         }
         __syncthreads();
-        for (int item = threadIdx.x; item < RPG * (D / 4); item += 64 * WPG * NG) {
-            const int rr = item / (D / 4), d4 = (item % (D / 4)) * 4;
+        // Each thread combines IT (row, 4-element) items; all slab reads are issued
+        // before any arithmetic so their LDS latencies overlap.
+        constexpr int NT = 64 * WPG * NG, IT = RPG * (D / 4) / NT;
+        static_assert(IT * NT == RPG * (D / 4), "merge items must divide evenly");
+        float2 ml[IT][NG];
+        f32x4 dv[IT][NG];
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int item = threadIdx.x + it * NT, rr = item / (D / 4), d4 = (item % (D / 4)) * 4;
+#pragma unroll
+            for (int gi = 0; gi < NG; gi++) {
+                const float *src = mslab + ((size_t)gi * RPG + rr) * MROW;
+                ml[it][gi] = *reinterpret_cast<const float2 *>(src + D);
+                dv[it][gi] = *reinterpret_cast<const f32x4 *>(src + d4);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < IT; it++) {
+            const int item = threadIdx.x + it * NT, rr = item / (D / 4), d4 = (item % (D / 4)) * 4;
             const int ttl = rr / p.G, gg = rr - ttl * p.G, tt = t_first + ttl;
-            if (ttl >= p.TQ || tt >= nb) continue;
             float mx = NEG_BIG;
 #pragma unroll
-            for (int gi = 0; gi < NG; gi++) mx = fmaxf(mx, mslab[((size_t)gi * RPG + rr) * MROW + D]);
+            for (int gi = 0; gi < NG; gi++) mx = fmaxf(mx, ml[it][gi].x);
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             float lsum = 0.0f;
 #pragma unroll
             for (int gi = 0; gi < NG; gi++) {
-                const float *src = mslab + ((size_t)gi * RPG + rr) * MROW;
-                const float wgt = fast_exp2(src[D] - mx);
-                lsum += src[D + 1] * wgt;
-                acc += *reinterpret_cast<const f32x4 *>(src + d4) * wgt;
+                const float wgt = fast_exp2(ml[it][gi].x - mx);
+                lsum += ml[it][gi].y * wgt;
+                acc += dv[it][gi] * wgt;
             }
+            if (ttl >= p.TQ || tt >= nb) continue;
             const float inv = 1.0f / lsum;
             uint16_t *orow = p.out + ((size_t)(tok0 + tt) * p.Hq + h * p.G + gg) * D + d4;
             *reinterpret_cast<u32x2 *>(orow) = (u32x2){pack_bf16x2(acc[0] * inv, acc[1] * inv),
