@@ -95,11 +95,12 @@ const char *ti_version(void);
 const char *ti_status_string(int status);
 
 /*
- * Bytes of workspace ti_attention needs for these shapes (0 for the prefill path).
+ * Bytes of workspace ti_attention needs for these shapes (0 when the call needs none).
  * Replaces attention_workspace(::TileBackend, q, k_pages) and decode_workspace
  * (src/ops/tile/attention.jl:279-284, :351-352; interface src/ops/interface.jl:275-280).
- * Depends only on host shape values, never on context length, so a captured graph
- * keeps a fixed workspace. Host only; writes the size to *bytes.
+ * Like the reference's, it depends only on the query shape (dtype, q_heads, num_seqs,
+ * max_query_len, path) and the cache, never on the block tables or context length, so
+ * a captured graph keeps a fixed workspace. Host only; writes the size to *bytes.
  */
 int ti_attention_workspace_bytes(const ti_attention_args *args, const ti_kv_cache *cache,
                                  size_t *bytes);

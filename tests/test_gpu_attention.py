@@ -158,6 +158,38 @@ def test_batched_ragged(gpu, path):
         check(ref, got[qsl[b]:qsl[b + 1]], True)
 
 
+# (head_dim, heads, kv_heads, page_size, start, n, causal, block-table width in pages)
+SPLIT_CASES = [(128, 32, 8, 16, 0, 16, True, 512),      # most splits hold no keys
+               (128, 32, 8, 16, 2048, 16, True, 160),   # the verify shape on a long prefix
+               (128, 32, 8, 16, 1500, 40, False, 160),  # non-causal, ragged last tile
+               (64, 12, 4, 16, 900, 12, True, 128)]
+
+
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_prefill_key_splits(gpu, case):
+    """The prefill kernel with its keys split across work-groups (partials merged by the
+    combine kernel), through AUTO and the forced prefill path; without a workspace the
+    prefill path runs unsplit (the reference runs its prefill kernel exactly when
+    attention! gets no workspace, src/ops/tile/attention.jl:354-366)."""
+    D, H, KVH, P, start, n, causal, width = case
+    c = make_case((D, H, KVH, P, start, n, causal), True, 1200 + start + n)
+    used = -(-(start + n) // P)
+    bt = np.zeros(width, np.int32)
+    bt[:used] = c["bt"][:used]
+    c["bt"] = bt
+    ref = exact(c)
+    q = dev(c["q"], torch.bfloat16)
+    k, v = dev(c["kp"], torch.bfloat16), dev(c["vp"], torch.bfloat16)
+    pos = torch.arange(start, start + n, dtype=torch.int32, device="cuda")
+    btd = torch.from_numpy(bt).cuda()
+    assert ti.workspace_bytes(q, k, path=ti.TI_PATH_PREFILL) > 0     # this shape splits
+    for path, with_ws in ((ti.TI_PATH_AUTO, True), (ti.TI_PATH_PREFILL, True), (ti.TI_PATH_PREFILL, False)):
+        ws = ti.attention_workspace(BE, q, k, path=path) if with_ws else None
+        out = torch.full_like(q, float("nan"))
+        ti.attention_(BE, out, ws, q, k, v, btd, pos, 1 / math.sqrt(D), causal, path=path)
+        check(ref, out.float().cpu().numpy(), True)
+
+
 def test_workspace_errors(gpu):
     c = make_case((128, 16, 8, 16, 100, 1, True), True, 1)
     q = dev(c["q"], torch.bfloat16)

@@ -30,15 +30,14 @@ FLAGS = [
 ]
 
 
-# MFMA accumulators in VGPRs (not AGPRs) avoid AGPR<->VGPR copies around the softmax
-# rescale; the wide decode variants need the AGPRs for their large accumulators.
-AGPR_FILES = {"pa_decode_wide.hip"}
+# MFMA accumulators in VGPRs (not AGPRs): no AGPR<->VGPR copies around the softmax
+# rescale.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    extra = [] if os.path.basename(src) in AGPR_FILES else ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-    cmd = [HIPCC, *FLAGS, *extra, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *VGPR_FORM, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

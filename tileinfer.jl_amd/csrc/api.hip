@@ -19,13 +19,18 @@ bool bad_cache(const ti_kv_cache *c, bool need_attention_dims) {
 bool bad_dtype(int dtype) { return dtype != TI_F32 && dtype != TI_BF16; }
 
 // Resolve the kernel family of an attention call: 0 generic (fp32), 1 decode, 2 prefill,
-// or a negative ti_status.
+// or a negative ti_status. AUTO takes the decode kernel for up to 32 packed query rows
+// (and for one query token with up to 64 heads per KV head); larger multi-token steps,
+// such as speculative verify, run faster on the prefill kernel with key splits, which
+// stages each K/V tile once in LDS for all its rows.
 int resolve_path(const ti_attention_args *a, const ti_kv_cache *c) {
     const int G = a->q_heads / c->kv_heads;
     if (a->dtype == TI_F32) return 0;
-    const bool decode_ok = G * a->max_query_len <= 64;
+    const int rows = G * a->max_query_len;
+    const bool decode_ok = rows <= 64;
+    const bool decode_auto = a->max_query_len <= 16 && (rows <= 32 || (a->max_query_len == 1 && decode_ok));
     switch (a->path) {
-        case TI_PATH_AUTO: return (a->max_query_len <= 16 && decode_ok) ? 1 : (G <= 64 ? 2 : -TI_ERR_UNSUPPORTED);
+        case TI_PATH_AUTO: return decode_auto ? 1 : (G <= 64 ? 2 : -TI_ERR_UNSUPPORTED);
         case TI_PATH_DECODE: return decode_ok ? 1 : -TI_ERR_UNSUPPORTED;
         case TI_PATH_PREFILL: return G <= 64 ? 2 : -TI_ERR_UNSUPPORTED;
         default: return -TI_ERR_INVALID_ARG;
@@ -72,6 +77,7 @@ int ti_attention_workspace_bytes(const ti_attention_args *a, const ti_kv_cache *
     const int path = resolve_path(a, c);
     if (path < 0) return -path;
     if (path == 1) *bytes = ti_plan_decode(a, c).bytes;
+    if (path == 2) *bytes = ti_plan_prefill(a, c, false).bytes;
     return TI_OK;
 }
 
@@ -82,7 +88,16 @@ int ti_attention(const ti_attention_args *a, const ti_kv_cache *c, void *stream)
     if (path < 0) return -path;
     hipStream_t s = (hipStream_t)stream;
     if (path == 0) return ti_launch_generic(a, c, s);
-    if (path == 2) return ti_launch_prefill(a, c, s);
+    if (path == 2) {
+        // The prefill path never requires a workspace (the reference runs its prefill
+        // kernel exactly when none is passed); without one it runs unsplit.
+        ti_prefill_plan pp = ti_plan_prefill(a, c, true);
+        if (pp.bytes > 0 && (!a->workspace || a->workspace_bytes < pp.bytes)) {
+            pp.splits = 1;
+            pp.bytes = 0;
+        }
+        return ti_launch_prefill(a, c, pp, s);
+    }
     const ti_decode_plan pl = ti_plan_decode(a, c);
     if (pl.bytes > 0 && (!a->workspace || a->workspace_bytes < pl.bytes)) return TI_ERR_WORKSPACE;
     return ti_launch_decode(a, c, pl, s);

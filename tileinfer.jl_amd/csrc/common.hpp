@@ -116,5 +116,22 @@ struct ti_decode_plan {
 ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c);
 int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_decode_plan &p,
                      hipStream_t s);
-int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s);
+// Merge split partials [B][Hk][splits][rows][D + 2] from a->workspace into a->out.
+int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows, int splits,
+                      hipStream_t s);
+
+struct ti_prefill_plan {
+    int wpg;         // waves per key group (32 packed rows each)
+    int ng;          // key groups per work-group
+    int splits;      // key splits across work-groups (partials merged by the combine kernel)
+    int TQ;          // query positions per q-tile
+    int qtiles;      // q-tiles per (sequence, KV head)
+    int rows;        // packed query rows G * max_query_len
+    size_t bytes;    // workspace bytes
+};
+// bound_keys: limit the key splits by the keys the block tables can hold (a launch); the
+// workspace query passes false and sizes for the most splits any block-table width allows.
+ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c, bool bound_keys);
+int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti_prefill_plan &p,
+                      hipStream_t s);
 int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s);

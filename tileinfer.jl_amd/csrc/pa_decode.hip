@@ -23,19 +23,38 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     if (t >= nb) return;
     const size_t stride = (size_t)p.M * (D + 2);
     const float *base = p.part + ((size_t)b * p.Hk + h) * p.splits * stride + (size_t)r * (D + 2);
-    float mx = NEG_BIG;
-#pragma unroll 8
-    for (int sp = 0; sp < p.splits; sp++) mx = fmaxf(mx, base[sp * stride + D]);
-    float acc[PER], lsum = 0.0f;
+    // Splits in batches of SB: every load of a batch (m, l and the row) is issued before
+    // any arithmetic, and batches merge online, so up to SB splits cost one round trip.
+    constexpr int SB = 8;
+    float mx = NEG_BIG, lsum = 0.0f, acc[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) acc[k] = 0.0f;
-#pragma unroll 8
-    for (int sp = 0; sp < p.splits; sp++) {
-        const float *src = base + sp * stride;
-        const float wgt = fast_exp2(src[D] - mx);
-        lsum += src[D + 1] * wgt;
+    for (int sp0 = 0; sp0 < p.splits; sp0 += SB) {
+        float2 ml[SB];
+        float dv[SB][PER];
 #pragma unroll
-        for (int k = 0; k < PER; k++) acc[k] += src[lane + 64 * k] * wgt;
+        for (int j = 0; j < SB; j++) {
+            const float *src = base + min(sp0 + j, p.splits - 1) * stride;
+            ml[j] = *reinterpret_cast<const float2 *>(src + D);
+#pragma unroll
+            for (int k = 0; k < PER; k++) dv[j][k] = src[lane + 64 * k];
+        }
+        float bm = mx;
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+            if (sp0 + j < p.splits) bm = fmaxf(bm, ml[j].x);
+        const float alpha = fast_exp2(mx - bm);
+        mx = bm;
+        lsum *= alpha;
+#pragma unroll
+        for (int k = 0; k < PER; k++) acc[k] *= alpha;
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+            const float wgt = sp0 + j < p.splits ? fast_exp2(ml[j].x - mx) : 0.0f;
+            lsum += ml[j].y * wgt;
+#pragma unroll
+            for (int k = 0; k < PER; k++) acc[k] += dv[j][k] * wgt;
+        }
     }
     const float inv = 1.0f / lsum;
     uint16_t *o = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
@@ -45,12 +64,13 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
 
 template <int D, bool INT8, bool PG16, int NW>
 void launch_decode_d(const DecodeParams &p, int rowb, dim3 grid, hipStream_t s) {
-    // 8-wave groups only for up to 32 packed rows (their merge slabs must fit the LDS);
-    // 48 and 64 rows run the variants built in pa_decode_wide.hip.
+    // 8-wave groups only for up to 32 packed rows (their merge slabs must fit the LDS).
+    // 33-64 rows: 4-wave groups of two wave pairs, each pair splitting the rows over the
+    // same keys (32 rows per wave keeps the accumulators in VGPRs at 2 waves per SIMD).
     switch (rowb) {
-        case 1: decode_kernel<D, 1, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
-        case 2: decode_kernel<D, 2, INT8, PG16, NW><<<grid, NW * 64, 0, s>>>(p); break;
-        default: ti_launch_decode_wide(p, D, rowb, INT8, PG16, grid, s); break;
+        case 1: decode_kernel<D, 1, INT8, PG16, NW, 1><<<grid, NW * 64, 0, s>>>(p); break;
+        case 2: decode_kernel<D, 2, INT8, PG16, NW, 1><<<grid, NW * 64, 0, s>>>(p); break;
+        default: decode_kernel<D, 2, INT8, PG16, 4, 2><<<grid, 256, 0, s>>>(p); break;
     }
 }
 
@@ -146,8 +166,22 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
         else launch_decode_p<64, false>(p, rowb, pl.waves, grid, s);
     }
     if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
-    if (pl.splits == 1) return TI_OK;
-    dim3 cgrid((pl.rows + 3) / 4, c->kv_heads, a->num_seqs);
+    return pl.splits == 1 ? TI_OK : ti_launch_combine(a, c, pl.rows, pl.splits, s);
+}
+
+int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows, int splits,
+                      hipStream_t s) {
+    DecodeParams p{};
+    p.out = (uint16_t *)a->out;
+    p.part = (float *)a->workspace;
+    p.qsl = a->query_start_loc;
+    p.Hk = c->kv_heads;
+    p.Hq = a->q_heads;
+    p.G = a->q_heads / c->kv_heads;
+    p.nmax = a->max_query_len;
+    p.M = rows;
+    p.splits = splits;
+    dim3 cgrid((rows + 3) / 4, c->kv_heads, a->num_seqs);
     if (c->head_dim == 128) combine_kernel<128><<<cgrid, 256, 0, s>>>(p);
     else combine_kernel<64><<<cgrid, 256, 0, s>>>(p);
     return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;

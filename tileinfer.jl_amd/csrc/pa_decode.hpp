@@ -183,13 +183,14 @@ __device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodePara
     }
 }
 
-template <int D, int ROWB, bool INT8, bool PG16, int NW>
+template <int D, int ROWB, bool INT8, bool PG16, int NW, int RS>
 __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     constexpr int NKB = D / 32;          // 32-wide head-dim blocks (QK MFMAs per tile)
     constexpr int NDT = D / 16;          // 16-wide head-dim tiles (PV MFMAs per tile)
     constexpr int CPR = D / 8;           // 8-element chunks per V row
     constexpr int KPL = 16 * CPR / 64;   // keys per lane in the V load (4 for D=128)
-    constexpr int MP = ROWB * 16;        // padded rows
+    constexpr int MP = ROWB * 16;        // padded rows per wave
+    constexpr int NKW = NW / RS;         // waves splitting the keys (RS row slices each)
 
     // Per-wave transposed V tiles during the key loop; afterwards the same LDS holds each
     // wave's (O, m, l) slab for the merge (rows of D + 4 floats, 16-B aligned).
@@ -204,6 +205,9 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
     const int r16 = lane & 15, kg = lane >> 4;
+    // RS = 2: waves pair up on the same keys, wave w holding rows MP*(w%2) .. + MP.
+    const int rslice = RS == 2 ? (w & 1) : 0, kw = RS == 2 ? (w >> 1) : w;
+    const int row0 = rslice * MP;
     const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
     const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
@@ -223,7 +227,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     int qpos[ROWB];
 #pragma unroll
     for (int rb = 0; rb < ROWB; rb++) {
-        const int r = rb * 16 + r16, t = r / p.G, g = r - t * p.G;
+        const int r = row0 + rb * 16 + r16, t = r / p.G, g = r - t * p.G;
         const bool ok = r < p.M && t < nb;
         qpos[rb] = p.causal && ok ? start + t : len - 1;
         const uint16_t *qr = p.q + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
@@ -359,15 +363,6 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
             for (int rb = 0; rb < ROWB; rb++)
                 o[rb][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop[rb], o[rb][dt], 0, 0, 0);
         }
-        if constexpr (ROWB >= 3) {
-            // The 48/64-row variants accumulate in AGPRs. Pin the accumulators there at
-            // the end of each tile: otherwise the compiler carries a VGPR copy of all of
-            // them around the loop (for the rare rescale) and re-reads it every tile.
-#pragma unroll
-            for (int rb = 0; rb < ROWB; rb++)
-#pragma unroll
-                for (int dt = 0; dt < NDT; dt++) asm volatile("" : "+a"(o[rb][dt]));
-        }
     };
 
     // Two register sets, ping-ponged: the next group of TPI tiles is loading while the
@@ -376,7 +371,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     // unconditionally (past the last tile it re-reads that tile, unused) so the count of
     // loads in flight is static and each wait covers only the tiles in use.
     constexpr int TPI = INT8 ? 2 : 1;
-    constexpr int STRIDE = NW * TPI;
+    constexpr int STRIDE = NKW * TPI;
     TileRegs<D, INT8> ta[TPI], tb[TPI];
     auto ld = [&](TileRegs<D, INT8> (&t)[TPI], int jj) {
 #pragma unroll
@@ -388,7 +383,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
         for (int e = 0; e < TPI; e++)
             if (jj + e < j1) compute(t[e], jj + e);
     };
-    int j = j0 + TPI * w;
+    int j = j0 + TPI * kw;
     if (j < j1) {
         ld(ta, j);
         while (true) {
@@ -425,14 +420,15 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     const size_t unit = ((size_t)b * p.Hk + h) * p.splits + s;
     for (int item = threadIdx.x; item < p.M * (D / 4); item += NW * 64) {
         const int r = item / (D / 4), d4 = (item % (D / 4)) * 4;
+        const int rs = RS == 2 ? r / MP : 0, rr = r - rs * MP;   // row slice, row in slab
         float mx = NEG_BIG;
 #pragma unroll
-        for (int wi = 0; wi < NW; wi++) mx = fmaxf(mx, mslab[((size_t)wi * MP + r) * MROW + D]);
+        for (int wi = 0; wi < NKW; wi++) mx = fmaxf(mx, mslab[((size_t)(wi * RS + rs) * MP + rr) * MROW + D]);
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         float lsum = 0.0f;
 #pragma unroll
-        for (int wi = 0; wi < NW; wi++) {
-            const float *src = mslab + ((size_t)wi * MP + r) * MROW;
+        for (int wi = 0; wi < NKW; wi++) {
+            const float *src = mslab + ((size_t)(wi * RS + rs) * MP + rr) * MROW;
             const float wgt = fast_exp2(src[D] - mx);
             lsum += src[D + 1] * wgt;
             acc += *reinterpret_cast<const f32x4 *>(src + d4) * wgt;
@@ -461,5 +457,3 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
 
 }  // namespace ti_decode
 
-void ti_launch_decode_wide(const ti_decode::DecodeParams &p, int D, int rowb, bool int8, bool pg16,
-                           dim3 grid, hipStream_t s);

@@ -39,7 +39,8 @@ struct PrefillParams {
     const int8_t *lq;
     const float *ls, *smooth;
     const int32_t *positions, *qsl, *bt;
-    int bt_stride, num_pages, P, pshift, Hk, Hq, G, TQ, nmax, qtiles, causal;
+    float *part;                       // split partials [B][Hk][splits][M][D + 2]
+    int bt_stride, num_pages, P, pshift, Hk, Hq, G, TQ, nmax, qtiles, causal, splits, M;
     float scale_log2;
 };
 
@@ -268,7 +269,8 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     // Grid (Hk, qtiles, B): consecutive work-groups (spread round-robin over the 8 XCDs)
     // belong to different KV heads, so each head's K/V stays in one XCD's L2.
     const int h = blockIdx.x;
-    const int qt = p.qtiles - 1 - (int)blockIdx.y;   // heaviest tiles first
+    const int qt = p.qtiles - 1 - (int)blockIdx.y / p.splits;   // heaviest tiles first
+    const int split = (int)blockIdx.y % p.splits;
     const int b = blockIdx.z;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
     const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
@@ -278,10 +280,26 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     const int t_last = min(t_first + p.TQ, nb) - 1;
     const int kend = p.causal ? start + t_last + 1 : len;
     const int nkt = (kend + KT - 1) / KT;
-    const int steps = (nkt + NG - 1) / NG;                 // same for every group
+    // This work-group's split: key tiles [kt_lo, kt_hi) of the q-tile's nkt.
+    const int per = (nkt + p.splits - 1) / p.splits;
+    const int kt_lo = min(split * per, nkt), kt_hi = min(kt_lo + per, nkt);
+    const int steps = (kt_hi - kt_lo + NG - 1) / NG;       // same for every group
+    const size_t unit = ((size_t)b * p.Hk + h) * p.splits + split;
     const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
     Smem<D> &sm = smg[grp];
     const int mask_from = p.causal ? start + t_first : len - 1;
+    if (steps == 0) {
+        // A split with no keys (short sequence): neutral partials (m = -big, l = 0, acc = 0)
+        // that the combine weights to zero.
+        constexpr int RPGW = 32 * WPG;
+        for (int idx = threadIdx.x; idx < RPGW * (D + 2); idx += 64 * WPG * NG) {
+            const int rr = idx / (D + 2), c = idx - rr * (D + 2);
+            const int ttl = rr / p.G, gg = rr - ttl * p.G, tt = t_first + ttl;
+            if (ttl < p.TQ && tt < nb)
+                p.part[(unit * p.M + (size_t)tt * p.G + gg) * (D + 2) + c] = c == D ? NEG_BIG : 0.0f;
+        }
+        return;
+    }
 
     // This lane's query row (B operand of S^T = K Q^T): elements i*16 + kg*8 .. +8.
     const int r = wl * 32 + r32, tl = r / p.G, g = r - tl * p.G, t = t_first + tl;
@@ -391,26 +409,26 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     // last tile, never used) so the number of loads in flight is static and the waits
     // before each LDS store only cover the tile being stored.
     Stage<D, INT8, GT> s0, s1;
-    auto tile_of = [&](int i) { return grp + NG * i; };
+    auto tile_of = [&](int i) { return kt_lo + grp + NG * i; };
     // Page ids of the next tile to load, fetched one load ahead.
-    TilePages pnext = PG16 ? tile_pages(p, bt, min(tile_of(0), nkt - 1)) : TilePages{};
+    TilePages pnext = PG16 ? tile_pages(p, bt, min(tile_of(0), kt_hi - 1)) : TilePages{};
     auto ld = [&](Stage<D, INT8, GT> &stg, int i) {
-        load_tile<D, INT8, PG16, GT>(stg, p, bt, h, min(tile_of(i), nkt - 1), kend, gtid, pnext);
-        if (PG16) pnext = tile_pages(p, bt, min(tile_of(i + 1), nkt - 1));
+        load_tile<D, INT8, PG16, GT>(stg, p, bt, h, min(tile_of(i), kt_hi - 1), kend, gtid, pnext);
+        if (PG16) pnext = tile_pages(p, bt, min(tile_of(i + 1), kt_hi - 1));
     };
     ld(s0, 0);
     ld(s1, 1);
-    if (tile_of(0) < nkt) store_tile<D, INT8, GT>(s0, sm, 0, gtid, kend - tile_of(0) * KT);
+    if (tile_of(0) < kt_hi) store_tile<D, INT8, GT>(s0, sm, 0, gtid, kend - tile_of(0) * KT);
     __syncthreads();
     for (int i = 0; i < steps; i += 2) {
         ld(s0, i + 2);
-        if (tile_of(i) < nkt) compute(tile_of(i), 0);
-        if (tile_of(i + 1) < nkt) store_tile<D, INT8, GT>(s1, sm, 1, gtid, kend - tile_of(i + 1) * KT);
+        if (tile_of(i) < kt_hi) compute(tile_of(i), 0);
+        if (tile_of(i + 1) < kt_hi) store_tile<D, INT8, GT>(s1, sm, 1, gtid, kend - tile_of(i + 1) * KT);
         __syncthreads();
         if (i + 1 >= steps) break;
         ld(s1, i + 3);
-        if (tile_of(i + 1) < nkt) compute(tile_of(i + 1), 1);
-        if (tile_of(i + 2) < nkt) store_tile<D, INT8, GT>(s0, sm, 0, gtid, kend - tile_of(i + 2) * KT);
+        if (tile_of(i + 1) < kt_hi) compute(tile_of(i + 1), 1);
+        if (tile_of(i + 2) < kt_hi) store_tile<D, INT8, GT>(s0, sm, 0, gtid, kend - tile_of(i + 2) * KT);
         __syncthreads();
     }
 
@@ -462,6 +480,13 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
                 acc += dv[it][gi] * wgt;
             }
             if (ttl >= p.TQ || tt >= nb) continue;
+            if (p.splits > 1) {
+                // The split's partial for packed row tt * G + gg: (acc, m, l).
+                float *dst = p.part + (unit * p.M + (size_t)tt * p.G + gg) * (D + 2);
+                *reinterpret_cast<f32x4 *>(dst + d4) = acc;
+                if (d4 == 0) *reinterpret_cast<float2 *>(dst + D) = make_float2(mx, lsum);
+                continue;
+            }
             const float inv = 1.0f / lsum;
             uint16_t *orow = p.out + ((size_t)(tok0 + tt) * p.Hq + h * p.G + gg) * D + d4;
             *reinterpret_cast<u32x2 *>(orow) = (u32x2){pack_bf16x2(acc[0] * inv, acc[1] * inv),
@@ -470,6 +495,17 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         return;
     }
     if (!row_ok) return;
+    if (p.splits > 1) {
+        float *dst = p.part + (unit * p.M + (size_t)t * p.G + g) * (D + 2);
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; e4++)
+                *reinterpret_cast<f32x4 *>(dst + 32 * db + 8 * e4 + 4 * kg) =
+                    (f32x4){o[db][4 * e4], o[db][4 * e4 + 1], o[db][4 * e4 + 2], o[db][4 * e4 + 3]};
+        if (kg == 0) *reinterpret_cast<float2 *>(dst + D) = make_float2(m, l);
+        return;
+    }
     const float inv = 1.0f / l;
     uint16_t *orow = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
 #pragma unroll
@@ -507,7 +543,51 @@ void launch_prefill_d(const PrefillParams &p, int wpg, int ng, dim3 grid, hipStr
 
 }  // namespace
 
-int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s) {
+// Shape of a prefill launch: WPG waves (32 packed rows each) per key group, NG key groups
+// per work-group, and key splits across work-groups, chosen so small prefills and verify
+// steps still spread over the 256 CUs. Depends only on host shapes (the block-table
+// width bounds the keys), never on positions, so a captured graph stays valid.
+// TI_PREFILL_WPG / TI_PREFILL_GROUPS / TI_PREFILL_SPLITS override (tuning only).
+ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c, bool bound_keys) {
+    static const int forced_wpg = [] {
+        const char *e = getenv("TI_PREFILL_WPG");
+        return e ? atoi(e) : 0;
+    }();
+    static const int forced_ng = [] {
+        const char *e = getenv("TI_PREFILL_GROUPS");
+        return e ? atoi(e) : 0;
+    }();
+    static const int forced_splits = [] {
+        const char *e = getenv("TI_PREFILL_SPLITS");
+        return e ? atoi(e) : 0;
+    }();
+    ti_prefill_plan pl;
+    const int G = a->q_heads / c->kv_heads;
+    const long long pairs = (long long)c->kv_heads * a->num_seqs;
+    pl.wpg = (long long)((a->max_query_len + 128 / G - 1) / (128 / G)) * pairs >= 256 ? 4 : 2;
+    if (forced_wpg == 2 || forced_wpg == 4) pl.wpg = forced_wpg;
+    if (32 * pl.wpg < G) pl.wpg = 4;
+    pl.TQ = 32 * pl.wpg / G;
+    pl.qtiles = (a->max_query_len + pl.TQ - 1) / pl.TQ;
+    const long long wgs = (long long)pl.qtiles * pairs;
+    pl.ng = wgs >= 1024 ? 1 : (wgs >= 512 ? 2 : 4);
+    if (forced_ng == 1 || forced_ng == 2 || forced_ng == 4) pl.ng = forced_ng;
+    if (pl.wpg == 4 && pl.ng > 2) pl.ng = 2;   // 16 waves of this kernel do not fit one CU's registers
+    // Split the keys while work-groups are fewer than the CUs and every split keeps at
+    // least 4 steps per key group of the longest context the block tables can hold.
+    const long long key_tiles = ((long long)a->block_table_stride * c->page_size + 31) / 32;
+    pl.splits = 1;
+    while (pl.splits < 16 && wgs * pl.splits < 256 &&
+           (!bound_keys || key_tiles / (2 * pl.splits) >= 4LL * pl.ng))
+        pl.splits *= 2;
+    if (forced_splits >= 1 && forced_splits <= 64) pl.splits = forced_splits;
+    pl.rows = G * a->max_query_len;
+    pl.bytes = pl.splits == 1 ? 0 : (size_t)pairs * pl.splits * pl.rows * (c->head_dim + 2) * sizeof(float);
+    return pl;
+}
+
+int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti_prefill_plan &pl,
+                      hipStream_t s) {
     PrefillParams p;
     p.q = (const uint16_t *)a->q;
     p.out = (uint16_t *)a->out;
@@ -529,28 +609,13 @@ int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, hipStrea
     p.nmax = a->max_query_len;
     p.causal = a->causal;
     p.scale_log2 = a->scale * LOG2E;
-    // Shape: WPG waves (32 packed rows each) per key group and NG key groups per
-    // work-group, chosen so small prefills still spread over the 256 CUs
-    // (TI_PREFILL_WPG / TI_PREFILL_GROUPS override, tuning only).
-    static const int forced_wpg = [] {
-        const char *e = getenv("TI_PREFILL_WPG");
-        return e ? atoi(e) : 0;
-    }();
-    static const int forced_ng = [] {
-        const char *e = getenv("TI_PREFILL_GROUPS");
-        return e ? atoi(e) : 0;
-    }();
-    const int G = p.G;
-    int wpg = G <= 64 && (long long)((a->max_query_len + 128 / G - 1) / (128 / G)) * c->kv_heads * a->num_seqs >= 256 ? 4 : 2;
-    if (forced_wpg == 2 || forced_wpg == 4) wpg = forced_wpg;
-    if (32 * wpg < G) wpg = 4;
-    p.TQ = 32 * wpg / G;
-    p.qtiles = (a->max_query_len + p.TQ - 1) / p.TQ;
-    const long long wgs = (long long)p.qtiles * c->kv_heads * a->num_seqs;
-    int ng = wgs >= 1024 ? 1 : (wgs >= 512 ? 2 : 4);
-    if (forced_ng == 1 || forced_ng == 2 || forced_ng == 4) ng = forced_ng;
-    if (wpg == 4 && ng > 2) ng = 2;   // 16 waves of this kernel do not fit one CU's registers
-    dim3 grid(c->kv_heads, p.qtiles, a->num_seqs);
+    p.part = (float *)a->workspace;
+    p.splits = pl.splits;
+    p.M = pl.rows;
+    p.TQ = pl.TQ;
+    p.qtiles = pl.qtiles;
+    const int wpg = pl.wpg, ng = pl.ng;
+    dim3 grid(c->kv_heads, p.qtiles * pl.splits, a->num_seqs);
     const bool int8 = c->kind == TI_KV_INT8;
     if (c->head_dim == 128) {
         if (int8) launch_prefill_d<128, true>(p, wpg, ng, grid, s);
@@ -559,5 +624,6 @@ int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, hipStrea
         if (int8) launch_prefill_d<64, true>(p, wpg, ng, grid, s);
         else launch_prefill_d<64, false>(p, wpg, ng, grid, s);
     }
-    return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
+    if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
+    return pl.splits > 1 ? ti_launch_combine(a, c, pl.rows, pl.splits, s) : TI_OK;
 }

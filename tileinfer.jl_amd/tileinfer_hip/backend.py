@@ -119,7 +119,7 @@ def _attention_args(out, q, block_tables, positions, scale, causal, path, num_se
 
 def workspace_bytes(q, k_pages, num_seqs: int = 1, max_query_len: Optional[int] = None,
                     path: int = _lib.TI_PATH_AUTO) -> int:
-    """Bytes of split-KV scratch ti_attention needs (0 for the prefill path)."""
+    """Bytes of split-KV scratch ti_attention needs for these query shapes (0 for none)."""
     # A shape-only query: the library validates and sizes, it never dereferences pointers.
     c = KVCache()
     if isinstance(k_pages, Int8Pages):
