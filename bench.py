@@ -160,7 +160,9 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", default="", help="comma list: decode,prefill,int8,verify,kvwrite")
+    ap.add_argument("--only", default="",
+                    help="comma list: decode,verify,int8,prefill (= prefill512,chunked),kvwrite; "
+                         "'none' runs the headline only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy a 512 MiB buffer 5 times (reference for rocprof byte counters)")
     args = ap.parse_args()
@@ -233,8 +235,8 @@ def main():
                                                      "pct_hbm_peak": round(100 * b8 / ms8 / 1e6 / HBM_PEAK_GBS, 1)}
         del s8
     torch.cuda.empty_cache()
-    if want("prefill"):
-        for start, n in ((0, 512), (1024, 512)):
+    for start, n, leg in ((0, 512, "prefill512"), (1024, 512, "chunked")):
+        if want("prefill") or want(leg):
             sp = decode_setup(1, start + n, n, Hq, Hk, D, P, 1, gen)
             msp = time_graph(lambda i: decode_call(sp, i, scale))
             visited = n * start + n * (n + 1) // 2
