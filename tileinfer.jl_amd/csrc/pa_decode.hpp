@@ -5,9 +5,10 @@
 //
 // Work decomposition. The G = Hq/Hk query heads that share a KV head, times the n query
 // tokens of the step, are packed into M = G*n query rows (row r = g + G t, as the
-// reference's packed tile). One work-group (4 waves) handles one (sequence, KV head,
-// split); a split is a contiguous range of 16-key tiles of the sequence, and the waves of
-// the group take every 4th tile of it, each with its own online-softmax state. The grid
+// reference's packed tile). One work-group (NW = 4 or 8 waves) handles one (sequence, KV
+// head, split); a split is a contiguous range of 16-key tiles of the sequence, and the
+// waves of the group take every NW-th tile of it, each with its own online-softmax state
+// (RS = 2: pairs of waves take the same tiles, each holding half of the rows). The grid
 // depends only on host shapes (B, Hk, splits), never on the context length, so a captured
 // graph stays valid as sequences grow; splits that get no keys write a neutral partial.
 //

@@ -7,20 +7,22 @@
 // keys 0 .. start + t; with causal = 0 it sees all start + n keys (attention.jl:155-157).
 // Chunked prefill over a cached prefix is the same kernel with start > 0.
 //
-// Work decomposition. A work-group (4 waves, 256 threads) owns 64 packed query rows of
-// one (sequence, KV head): the G query heads of the KV head times TQ = 64 / G consecutive
-// query positions, row r = g + G t as in the decode kernel, so every K/V tile loaded into
-// LDS serves all G heads. Query tiles are issued heaviest first (the last positions see
+// Work decomposition. A work-group is NG key groups of WPG waves. Each wave owns 32
+// packed query rows of one (sequence, KV head) — the G query heads of the KV head times
+// consecutive positions, row r = g + G t as in the decode kernel — so every K/V tile
+// loaded into LDS serves all G heads. The key groups split the q-tile's key tiles and
+// merge through LDS at the end; with key splits across work-groups (small grids), each
+// work-group covers a contiguous range of key tiles and writes Float32 partials that the
+// combine kernel merges. Query tiles are issued heaviest first (the last positions see
 // the most keys). Keys stream through LDS in 32-key tiles, double-buffered: global loads
-// of tile j+1 are in flight while the waves compute tile j. K is kept row-major (the A
-// operand of S^T = K Q^T), V transposed (the A operand of O^T = V^T P^T).
+// of later tiles are in flight while the waves compute the current one.
 //
-// Per wave (16 rows) and 32-key tile:
-//   S^T = K Q^T        2 x (D/32) v_mfma_f32_16x16x32_bf16 (two 16-key blocks)
-//   online softmax     exp2 domain, lane-local per row + two xor shuffles for the max
-//   O^T += V^T P^T     D/16 v_mfma_f32_16x16x32_bf16; P^T is the S^T registers of both
-//                      key blocks rounded to bf16 (k slots: keys 4k..4k+3 and 16+4k..+3),
-//                      V^T read with the same key order.
+// Per wave (32 rows) and 32-key tile:
+//   S^T = K Q^T        D/16 v_mfma_f32_32x32x16_bf16 (K rows from LDS as the A operand)
+//   online softmax     exp2 domain, lane-local per row + one xor shuffle for the max
+//   O^T += V^T P^T     2 D/32 v_mfma_f32_32x32x16_bf16; P^T is the S^T registers rounded
+//                      to bf16, V^T is read from the row-major V tile by transposing
+//                      LDS reads (ds_read_b64_tr_b16).
 // INT8: keys and values enter LDS converted to bf16 (exact), their scales beside them; a
 // key's scale multiplies its scores, a value's scale its probability; queries are
 // multiplied by the keys' smoothing and rounded to bf16 (attention.jl:68-95).
