@@ -76,7 +76,7 @@ void launch_decode_d(const DecodeParams &p, int rowb, dim3 grid, hipStream_t s) 
 
 template <int D, bool INT8>
 void launch_decode_p(const DecodeParams &p, int rowb, int waves, dim3 grid, hipStream_t s) {
-    if (p.P % 16 == 0) {
+    if (p.P % 16 == 0 && p.pshift >= 0) {
         if (waves == 8) launch_decode_d<D, INT8, true, 8>(p, rowb, grid, s);
         else launch_decode_d<D, INT8, true, 4>(p, rowb, grid, s);
     } else {

@@ -91,7 +91,7 @@ struct TileRegs {
 };
 
 // Pool row of key position pos of KV head h. PG16: the 16-key tile lies in one page
-// (P % 16 == 0), so the caller passes the page's first row; otherwise a per-key lookup
+// (P a power of two >= 16), so the caller passes the page's first row; otherwise a per-key lookup
 // with the position clamped into the sequence (rows past len are never used unmasked).
 struct RowMap {
     const int32_t *bt;
@@ -107,11 +107,11 @@ struct RowMap {
         const int pg = page_of(bt, page_index(pos), num_pages);
         return ((long long)pg * Hk + h) * P + page_offset(pos);
     }
-    // pos wave-uniform: scalar block-table load
+    // pos wave-uniform, P a power of two: scalar block-table load, shifts only
     __device__ __forceinline__ long long row_s(int pos) const {
         pos = min(pos, len - 1);
-        const int pg = page_of_s(bt, page_index(pos), num_pages);
-        return ((long long)pg * Hk + h) * P + page_offset(pos);
+        const int pg = page_of_s(bt, pos >> pshift, num_pages);
+        return ((long long)pg * Hk + h) * P + (pos & (P - 1));
     }
 };
 

@@ -76,9 +76,9 @@ __device__ __forceinline__ long long key_row(const PrefillParams &p, const int32
     return ((long long)pg * p.Hk + h) * p.P + off;
 }
 
-// Rows of a tile's keys. PG16 (P % 16 == 0): each 16-key half of the tile lies in one
-// page, found with a scalar block-table load; key k's row is half_row[k / 16] + k % 16.
-// Otherwise a per-key lookup (vector loads).
+// Rows of a tile's keys. PG16 (P a power of two >= 16): each 16-key half of the tile lies
+// in one page, found with a scalar block-table load and shifts (no division); key k's row
+// is half_row[k / 16] + k % 16. Otherwise a per-key lookup (vector loads).
 template <bool PG16>
 struct TileRows {
     long long half_row[2];
@@ -91,8 +91,7 @@ struct TileRows {
 #pragma unroll
             for (int x = 0; x < 2; x++) {
                 const int pos = min(kt * KT + 16 * x, kend - 1);
-                const int idx = pp.pshift >= 0 ? pos >> pp.pshift : pos / pp.P;
-                const int off = pp.pshift >= 0 ? pos & (pp.P - 1) : pos % pp.P;
+                const int idx = pos >> pp.pshift, off = pos & (pp.P - 1);   // PG16: P is 2^pshift
                 const int pg = page_of_s(btp, idx, pp.num_pages);
                 half_row[x] = ((long long)pg * pp.Hk + hh) * pp.P + (off & ~15);
             }
@@ -130,7 +129,7 @@ __device__ __forceinline__ TilePages tile_pages(const PrefillParams &p, const in
 #pragma unroll
     for (int x = 0; x < 2; x++) {
         const int pos = kt * KT + 16 * x;
-        const int idx = min(p.pshift >= 0 ? pos >> p.pshift : pos / p.P, p.bt_stride - 1);
+        const int idx = min(pos >> p.pshift, p.bt_stride - 1);   // only PG16 tiles: P = 2^pshift
         tp.pg[x] = page_of_s(bt, idx, p.num_pages);
     }
     return tp;
@@ -153,7 +152,7 @@ __device__ __forceinline__ void load_tile(Stage<D, INT8, GT> &st, const PrefillP
 #pragma unroll
         for (int x = 0; x < 2; x++) {
             const int pos = kt * KT + 16 * x;
-            const int off = p.pshift >= 0 ? pos & (p.P - 1) : pos % p.P;
+            const int off = pos & (p.P - 1);
             base[x] = (((long long)tp.pg[x] * p.Hk + h) * p.P + off) * D;
         }
 #pragma unroll
@@ -340,7 +339,8 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     const int c16 = lane >> 4, s16 = lane & 15;
     const int tr_row = 4 * (c16 >> 1) + (s16 >> 2), tr_col = 16 * (c16 & 1) + 4 * (s16 & 3);
 
-    auto compute = [&](int kt, int buf) {
+    auto compute = [&](int kt, int buf, auto &&issue_loads) {
+        issue_loads();
         // Two independent accumulation chains (even / odd head-dim blocks) halve the
         // dependent-MFMA latency of the score tile.
         f32x16 sc, sc2;
@@ -354,10 +354,22 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qreg[i], sc, 0, 0, 0);
             sc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qreg[i + 1], sc2, 0, 0, 0);
         }
+        // Spread the next tile's global loads between the score MFMAs and their K reads,
+        // so the CU's load path drains while the matrix cores run.
+#pragma unroll
+        for (int i = 0; i < NQB; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);   // one global load
+            __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // one LDS read
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);   // one MFMA
+        }
         sc += sc2;
         // Online softmax in the exp2 domain: p = exp2(s * scale - m) with m the running
         // (scaled) reference max; the tile max is taken on raw scores (scale > 0).
-        const bool need_mask = kt * KT + KT - 1 > mask_from;
+        // A tile past this group's keys (its last step) runs the score stage on whatever
+        // the buffer holds, fully masked, so the next loads and the score MFMAs share one
+        // scheduling region; its PV stage is skipped.
+        const bool valid = kt < kt_hi;
+        const bool need_mask = !valid || kt * KT + KT - 1 > mask_from;
         float x[16];
         float mt = -INFINITY;
 #pragma unroll
@@ -367,7 +379,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
             if (INT8) v *= sm.sk[buf][key];
             if (need_mask) {
                 const int kpos = kt * KT + key;
-                v = (kpos <= qpos && kpos < kend) ? v : -INFINITY;
+                v = (valid && kpos <= qpos && kpos < kend) ? v : -INFINITY;
             }
             x[e] = v;
             mt = fmaxf(mt, v);
@@ -395,6 +407,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         for (int hh = 0; hh < 2; hh++)
             pb[hh] = as_bf16x8((u32x4){pack_bf16x2(pe[8 * hh + 0], pe[8 * hh + 1]), pack_bf16x2(pe[8 * hh + 2], pe[8 * hh + 3]),
                                        pack_bf16x2(pe[8 * hh + 4], pe[8 * hh + 5]), pack_bf16x2(pe[8 * hh + 6], pe[8 * hh + 7])});
+        if (!valid) return;
         const uint16_t *vb = &sm.v[buf][tr_row * Smem<D>::VROW + tr_col];
 #pragma unroll
         for (int db = 0; db < NDB; db++)
@@ -423,13 +436,11 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     if (tile_of(0) < kt_hi) store_tile<D, INT8, GT>(s0, sm, 0, gtid, kend - tile_of(0) * KT);
     __syncthreads();
     for (int i = 0; i < steps; i += 2) {
-        ld(s0, i + 2);
-        if (tile_of(i) < kt_hi) compute(tile_of(i), 0);
+        compute(tile_of(i), 0, [&] { ld(s0, i + 2); });
         if (tile_of(i + 1) < kt_hi) store_tile<D, INT8, GT>(s1, sm, 1, gtid, kend - tile_of(i + 1) * KT);
         __syncthreads();
         if (i + 1 >= steps) break;
-        ld(s1, i + 3);
-        if (tile_of(i + 1) < kt_hi) compute(tile_of(i + 1), 1);
+        compute(tile_of(i + 1), 1, [&] { ld(s1, i + 3); });
         if (tile_of(i + 2) < kt_hi) store_tile<D, INT8, GT>(s0, sm, 0, gtid, kend - tile_of(i + 2) * KT);
         __syncthreads();
     }
@@ -539,7 +550,7 @@ void launch_prefill_g(const PrefillParams &p, int wpg, int ng, dim3 grid, hipStr
 
 template <int D, bool INT8>
 void launch_prefill_d(const PrefillParams &p, int wpg, int ng, dim3 grid, hipStream_t s) {
-    if (p.P % 16 == 0) launch_prefill_g<D, INT8, true>(p, wpg, ng, grid, s);
+    if (p.P % 16 == 0 && p.pshift >= 0) launch_prefill_g<D, INT8, true>(p, wpg, ng, grid, s);
     else launch_prefill_g<D, INT8, false>(p, wpg, ng, grid, s);
 }
 
