@@ -30,7 +30,9 @@ REF_CASES = [(128, 16, 8, 64, 1023, 1, True), (128, 16, 8, 64, 63, 2, True),
 EXTRA_CASES = [(128, 32, 8, 16, 1500, 1, True), (128, 32, 8, 16, 4000, 16, True),
                (128, 32, 8, 4, 37, 9, True), (128, 8, 8, 16, 77, 3, True),
                (128, 64, 8, 16, 120, 8, True), (64, 8, 2, 32, 0, 1, True),
-               (128, 32, 8, 16, 1024, 512, True), (128, 16, 8, 16, 0, 100, False)]
+               (128, 32, 8, 16, 1024, 512, True), (128, 16, 8, 16, 0, 100, False),
+               # 48-token pages: whole 16-key tiles per page, but not a power of two
+               (128, 32, 8, 48, 700, 5, True), (128, 16, 8, 48, 100, 200, True)]
 
 
 def dev(x, dtype):
