@@ -170,7 +170,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="",
-                    help="comma list: decode,verify,int8,prefill (= prefill512,chunked),kvwrite; "
+                    help="comma list: decode,verify,int8,prefill (= prefill512,chunked,prefill4096),kvwrite; "
                          "'none' runs the headline only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy a 512 MiB buffer 5 times (reference for rocprof byte counters)")
@@ -252,14 +252,15 @@ def main():
                                                      "pct_hbm_peak": round(100 * b8 / ms8 / 1e6 / HBM_PEAK_GBS, 1)}
         del s8
     torch.cuda.empty_cache()
-    for start, n, leg in ((0, 512, "prefill512"), (1024, 512, "chunked")):
+    for start, n, leg in ((0, 512, "prefill512"), (1024, 512, "chunked"), (0, 4096, "prefill4096")):
         if want("prefill") or want(leg):
             sp = decode_setup(1, start + n, n, Hq, Hk, D, P, 1, gen, cold=False)
             msp = time_graph(lambda i: decode_call(sp, i, scale))
             visited = n * start + n * (n + 1) // 2
             flops = 4 * D * Hq * visited
             tf = flops / (msp * 1e-3) / 1e12
-            key = "prefill_512" if start == 0 else "chunked_prefill_512_on_1024"
+            key = {"prefill512": "prefill_512", "chunked": "chunked_prefill_512_on_1024",
+                   "prefill4096": "prefill_4096"}[leg]
             extra[key] = {"us": round(msp * 1e3, 2), "TFLOP/s": round(tf, 1),
                           "pct_mfma_peak": round(100 * tf / BF16_PEAK_TFLOPS, 2), "gflop": round(flops / 1e9, 3)}
             log(f"{key}: {msp * 1e3:.1f} us, {tf:.1f} TFLOP/s")
