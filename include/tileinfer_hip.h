@@ -130,6 +130,17 @@ int ti_store_kv(int dtype, const ti_kv_cache *cache, const void *k, const void *
                 const int32_t *slots, int n, void *stream);
 
 /*
+ * RMS normalization of `rows` rows of `hidden` elements: y = rnd(rnd(x inv_rms) w) with
+ * inv_rms = 1 / sqrt(sum x^2 / hidden + eps) in Float32, rnd = round to T (y may alias x).
+ * Replaces rmsnorm!(::TileBackend, y, x, w, eps) (src/ops/tile/norm.jl:31-38; interface
+ * src/ops/interface.jl:118-122), the q/k norm of the generic attention_inputs! chain
+ * (interface.jl:175). Per-head rows (hidden <= 128) are bit-identical to the norm inside
+ * ti_attention_inputs. x, y: [rows][hidden], w: [hidden], all in dtype.
+ */
+int ti_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int hidden, float eps,
+               void *stream);
+
+/*
  * Rotary embedding ("rotate half") of x [n][heads][D] into y at 0-based positions,
  * rounding to T after every operation as the reference does.
  * Replaces rope!(::TileBackend, y, x, cos, sin, positions)

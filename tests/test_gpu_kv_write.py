@@ -141,6 +141,60 @@ def test_attention_inputs(gpu, bf16, qk_norm):
         assert np.allclose(kq.layer_scale.cpu().numpy(), ls, rtol=1e-2)
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_inputs_norm_equals_unfused_chain(gpu, bf16, D):
+    """Fused q/k RMSNorm + RoPE + KV write == rmsnorm_ -> rope -> store_kv_ run one by one,
+    bit-identical (test/ops/tile.jl:109-146; the generic chain src/ops/interface.jl:169-179),
+    into a dense and an INT8 cache."""
+    nq, nkv, P, pages, L = 8, 2, 16, 6, 64
+    g = rng(480 + 2 * D + bf16)
+    positions = np.array([3, 17, 18, 40, 0], np.int32)
+    slots = np.array([13, 14, 15, 16, 70], np.int32)
+    n = len(positions)
+    c, s, table = _table(g, D, L, bf16)
+    qkv = randn(g, n, nq + 2 * nkv, D, bf16=bf16)
+    qn, kn = randn(g, D, bf16=bf16), randn(g, D, bf16=bf16)
+    pos_d, slots_d = torch.from_numpy(positions).cuda(), torch.from_numpy(slots).cuda()
+    qkv_d, qn_d, kn_d = dev(qkv, bf16), dev(qn, bf16), dev(kn, bf16)
+
+    q = torch.zeros((n, nq, D), dtype=DT[bf16], device="cuda")
+    kp = torch.zeros((pages, nkv, P, D), dtype=DT[bf16], device="cuda")
+    vp = torch.zeros_like(kp)
+    ti.attention_inputs_(BE, q, kp, vp, qkv_d, qn_d, kn_d, table, pos_d, slots_d, 1e-6)
+
+    qs = ti.rmsnorm(BE, qkv_d[:, :nq].contiguous(), qn_d, 1e-6)
+    ks = ti.rmsnorm(BE, qkv_d[:, nq:nq + nkv].contiguous(), kn_d, 1e-6)
+    vv = qkv_d[:, nq + nkv:].contiguous()
+    q2 = ti.rope(BE, qs, table.cos, table.sin, pos_d)
+    k2 = ti.rope(BE, ks, table.cos, table.sin, pos_d)
+    kp2, vp2 = torch.zeros_like(kp), torch.zeros_like(kp)
+    ti.store_kv_(BE, kp2, vp2, k2, vv, slots_d)
+    assert torch.equal(q, q2) and torch.equal(kp, kp2) and torch.equal(vp, vp2)
+
+    cs = smoothing(g, D)
+    kq, vq = ti.int8_kv_pools(D, P, nkv, pages, key_smoothing=torch.from_numpy(cs))
+    kq2, vq2 = ti.int8_kv_pools(D, P, nkv, pages, key_smoothing=torch.from_numpy(cs))
+    ti.attention_inputs_(BE, torch.zeros_like(q), kq, vq, qkv_d, qn_d, kn_d, table, pos_d, slots_d, 1e-6)
+    ti.store_kv_(BE, kq2, vq2, k2, vv, slots_d)
+    assert torch.equal(kq.layer_q, kq2.layer_q) and torch.equal(kq.layer_scale, kq2.layer_scale)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("H", [128, 100, 2560])
+def test_rmsnorm(gpu, bf16, H):
+    """rmsnorm_ rows (src/ops/tile/norm.jl:5-38) against the formula in float64 with the
+    reference's rounding points: within one rounding of T (the Float32 sum order differs)."""
+    g = rng(900 + H + bf16)
+    x = randn(g, 7, H, bf16=bf16)
+    w = randn(g, H, bf16=bf16)
+    y = ti.rmsnorm(BE, dev(x, bf16), dev(w, bf16), 1e-6).float().cpu().numpy()
+    inv = 1.0 / np.sqrt((x.astype(np.float64) ** 2).sum(1, keepdims=True) / H + 1e-6)
+    rnd = orc.bf16_round if bf16 else (lambda a: a.astype(np.float32))
+    ref = rnd(rnd((x * inv).astype(np.float32)) * w[None, :])
+    assert ulps(ref, y) <= 1 if bf16 else np.allclose(ref, y, rtol=1e-5, atol=1e-6)
+
+
 def test_out_of_range_slots_are_skipped(gpu):
     D, P, H, pages = 64, 4, 2, 3
     k = torch.ones((3, H, D), dtype=torch.bfloat16, device="cuda")

@@ -124,6 +124,14 @@ int ti_rope(int dtype, void *y, const void *x, const void *cos_table, const void
                           head_dim, (hipStream_t)stream);
 }
 
+int ti_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int hidden, float eps,
+               void *stream) {
+    if (bad_dtype(dtype) || rows < 0 || hidden <= 0 || !(eps >= 0.0f)) return TI_ERR_INVALID_ARG;
+    if (rows == 0) return TI_OK;
+    if (!y || !x || !w) return TI_ERR_INVALID_ARG;
+    return ti_launch_rmsnorm(dtype, y, x, w, rows, hidden, eps, (hipStream_t)stream);
+}
+
 int ti_attention_inputs(int dtype, void *q_out, const ti_kv_cache *c, const void *qkv,
                         const void *q_norm, const void *k_norm, const void *cos_sin,
                         int table_len, const int32_t *positions, const int32_t *slots, int n,

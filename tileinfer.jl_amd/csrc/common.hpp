@@ -97,6 +97,8 @@ __device__ __forceinline__ int page_of_s(const int32_t *bt, int idx, int num_pag
 }  // namespace ti
 
 // Launchers implemented per kernel file, dispatched by api.hip.
+int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int H, float eps,
+                      hipStream_t s);
 int ti_launch_rope(int dtype, void *y, const void *x, const void *cos_t, const void *sin_t,
                    int table_len, const int32_t *positions, int n, int heads, int D,
                    hipStream_t s);

@@ -125,6 +125,41 @@ __global__ void __launch_bounds__(64) store_kv_int8_kernel(int8_t *__restrict__ 
     quantize_store(x, D, lq + half_q, ls + half_s, (size_t)row);
 }
 
+// ---- rmsnorm (src/ops/tile/norm.jl:5-38; reference src/ops/interface.jl:118-122) ----
+// y = rnd(rnd(x inv_rms) w), inv_rms = 1 / sqrt(sum x^2 / H + eps) in Float32; one wave
+// per row of H elements. Rows of up to 128 elements (even H) are reduced with the fused
+// attention-input kernel's pairing (lane i holds elements i and i + H/2), so a per-head
+// norm here is bit-identical to the one inside that kernel.
+template <typename T>
+__global__ void __launch_bounds__(64) rmsnorm_kernel(T *__restrict__ y, const T *__restrict__ x,
+                                                      const T *__restrict__ w, int H, float eps) {
+    using E = Elt<T>;
+    const size_t base = (size_t)blockIdx.x * H;
+    const int lane = threadIdx.x;
+    if (H <= 128 && (H & 1) == 0) {
+        const int half = H / 2;
+        const bool on = lane < half;
+        const float a = on ? E::ld(x, base + lane) : 0.0f;
+        const float b = on ? E::ld(x, base + lane + half) : 0.0f;
+        const float ss = wave_sum(a * a + b * b);
+        const float inv_rms = __frcp_rn(__fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), eps)));
+        if (on) {
+            E::st(y, base + lane, E::rnd(E::rnd(a * inv_rms) * E::ld(w, lane)));
+            E::st(y, base + lane + half, E::rnd(E::rnd(b * inv_rms) * E::ld(w, lane + half)));
+        }
+        return;
+    }
+    float acc = 0.0f;
+    for (int i = lane; i < H; i += WAVE) {
+        const float v = E::ld(x, base + i);
+        acc = acc + v * v;
+    }
+    const float ss = wave_sum(acc);
+    const float inv_rms = __frcp_rn(__fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), eps)));
+    for (int i = lane; i < H; i += WAVE)
+        E::st(y, base + i, E::rnd(E::rnd(E::ld(x, base + i) * inv_rms) * E::ld(w, i)));
+}
+
 // ---- fused attention inputs (src/ops/tile/fused.jl:15-92) ----
 // Grid (n, nq + nkv), one wave per (token, head). Lane i < D/2 owns the rotary pair
 // (i, i + D/2). Heads j < nq are queries -> q_out; the others are KV head h = j - nq:
@@ -215,6 +250,15 @@ __global__ void __launch_bounds__(64) attention_inputs_kernel(
 }
 
 }  // namespace
+
+int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int H, float eps,
+                      hipStream_t s) {
+    if (dtype == TI_BF16)
+        rmsnorm_kernel<uint16_t><<<rows, 64, 0, s>>>((uint16_t *)y, (const uint16_t *)x, (const uint16_t *)w, H, eps);
+    else
+        rmsnorm_kernel<float><<<rows, 64, 0, s>>>((float *)y, (const float *)x, (const float *)w, H, eps);
+    return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
+}
 
 int ti_launch_rope(int dtype, void *y, const void *x, const void *cos_t, const void *sin_t,
                    int table_len, const int32_t *positions, int n, int heads, int D,

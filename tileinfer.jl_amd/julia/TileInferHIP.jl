@@ -121,6 +121,14 @@ function TileInfer.store_kv!(::HipBackend, k_pages, v_pages, k::ROCArray{T,3}, v
     return nothing
 end
 
+# rmsnorm!(::TileBackend, y, x, w, eps): src/ops/tile/norm.jl:31-38
+function TileInfer.rmsnorm!(::HipBackend, y::ROCArray{T}, x::ROCArray{T}, w::ROCVector{T}, eps::Real) where {T}
+    H = size(x, 1)
+    check(ccall((:ti_rmsnorm, LIB), Cint, (Cint, Ptr{Cvoid}, Ptr{Cvoid}, Ptr{Cvoid}, Cint, Cint, Cfloat, Ptr{Cvoid}),
+                dtype_code(T), vptr(y), vptr(x), vptr(w), length(x) ÷ H, H, Float32(eps), stream().stream))
+    return y
+end
+
 # rope!(::TileBackend, ...): src/ops/tile/elementwise.jl:29-36
 function TileInfer.rope!(::HipBackend, y::ROCArray{T,3}, x::ROCArray{T,3}, cos::ROCArray{T,2},
                          sin::ROCArray{T,2}, positions::ROCVector{Int32}) where {T}
@@ -149,7 +157,7 @@ end
 
 TileInfer.supports_graphs(::HipBackend) = true
 TileInfer.has_kernel(::HipBackend, op) = op in (TileInfer.attention!, TileInfer.attention,
-                                               TileInfer.store_kv!, TileInfer.rope!,
+                                               TileInfer.store_kv!, TileInfer.rmsnorm!, TileInfer.rope!,
                                                TileInfer.attention_inputs!)
 
 export HipBackend

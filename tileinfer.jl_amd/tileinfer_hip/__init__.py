@@ -6,7 +6,7 @@ Host-side mirror of the reference's op interface (src/ops/interface.jl) and KV l
 from ._lib import (ArgumentError, TileInferError, WorkspaceError, TI_PATH_AUTO, TI_PATH_DECODE,
                    TI_PATH_PREFILL, EXPORTS, LIB_PATH, load as load_library)
 from .backend import (HipBackend, attention, attention_, attention_inputs_, attention_workspace,
-                      has_kernel, kv_cache_struct, paged_attention_, rope, rope_, store_kv_,
+                      has_kernel, kv_cache_struct, paged_attention_, rmsnorm, rmsnorm_, rope, rope_, store_kv_,
                       supports_graphs, workspace_bytes)
 from .kv import (DEFAULT_PAGE_SIZE, BlockManager, Int8Pages, OutOfPagesError, PagedKVCache,
                  Sequence, bytes_per_token, int8_kv_pools, key_smoothing, layer_arrays, release,

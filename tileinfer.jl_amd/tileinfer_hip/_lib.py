@@ -19,7 +19,7 @@ TI_PATH_AUTO, TI_PATH_DECODE, TI_PATH_PREFILL = 0, 1, 2
 
 # Every symbol include/tileinfer_hip.h declares.
 EXPORTS = ("ti_version", "ti_status_string", "ti_attention_workspace_bytes", "ti_attention",
-           "ti_store_kv", "ti_rope", "ti_attention_inputs")
+           "ti_store_kv", "ti_rmsnorm", "ti_rope", "ti_attention_inputs")
 
 
 class KVCache(ctypes.Structure):
@@ -65,6 +65,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.ti_attention.argtypes = [P(AttentionArgs), P(KVCache), vp]
     L.ti_store_kv.restype = i32
     L.ti_store_kv.argtypes = [i32, P(KVCache), vp, vp, vp, i32, vp]
+    L.ti_rmsnorm.restype = i32
+    L.ti_rmsnorm.argtypes = [i32, vp, vp, vp, i32, i32, ctypes.c_float, vp]
     L.ti_rope.restype = i32
     L.ti_rope.argtypes = [i32, vp, vp, vp, vp, i32, vp, i32, i32, i32, vp]
     L.ti_attention_inputs.restype = i32

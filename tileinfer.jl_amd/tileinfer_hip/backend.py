@@ -32,7 +32,7 @@ class HipBackend:
         return "HipBackend()"
 
 
-_OPS = {"attention", "attention!", "store_kv!", "rope", "rope!", "attention_inputs!"}
+_OPS = {"attention", "attention!", "store_kv!", "rmsnorm", "rmsnorm!", "rope", "rope!", "attention_inputs!"}
 
 
 def supports_graphs(be: HipBackend) -> bool:
@@ -205,6 +205,23 @@ def store_kv_(be: HipBackend, k_pages, v_pages, k, v, slots):
         raise ArgumentError("k/v/slots shapes do not match the pools")
     check(_lib.load().ti_store_kv(_dtype(k), ctypes.byref(c), _ptr(k), _ptr(v), _ptr(slots),
                                   k.shape[0], _stream(k)))
+
+
+def rmsnorm_(be: HipBackend, y, x, w, eps: float):
+    """rmsnorm!(::TileBackend, y, x, w, eps) (src/ops/tile/norm.jl:31-38): every row of the
+    last dimension of x normalized as rnd(rnd(x inv_rms) w). y may be x."""
+    _dev(y, x, w)
+    if y.shape != x.shape or y.dtype != x.dtype or w.dtype != x.dtype or w.dim() != 1 \
+            or w.shape[0] != x.shape[-1] or not (x.is_contiguous() and y.is_contiguous()):
+        raise ArgumentError("rmsnorm shapes/types mismatch")
+    H = x.shape[-1]
+    check(_lib.load().ti_rmsnorm(_dtype(x), _ptr(y), _ptr(x), _ptr(w), x.numel() // H, H, float(eps),
+                                 _stream(x)))
+    return y
+
+
+def rmsnorm(be: HipBackend, x, w, eps: float):
+    return rmsnorm_(be, torch.empty_like(x), x, w, eps)
 
 
 def rope_(be: HipBackend, y, x, cos, sin, positions):
