@@ -170,7 +170,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="",
-                    help="comma list: decode,verify,int8,prefill (= prefill512,chunked,prefill4096),kvwrite; "
+                    help="comma list: decode,fp32,verify,int8,prefill (= prefill512,chunked,prefill4096),kvwrite; "
                          "'none' runs the headline only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy a 512 MiB buffer 5 times (reference for rocprof byte counters)")
@@ -237,6 +237,25 @@ def main():
             bx = decode_bytes(Bx, L, 1, Hq, Hk, D, D * 2)
             extra[f"decode_b{Bx}"] = {"us": round(msx * 1e3, 2), "GB/s": round(bx / msx / 1e6, 1)}
             del sx
+    if want("fp32"):
+        # configs[0]'s shape on the fp32 path: B = 1, 16 query / 8 KV heads, 1024 positions
+        import tileinfer_hip as ti
+        L1, H1, K1 = 1024, 16, 8
+        copies = 32                                  # 8.4 MB per copy: cycle past the cache
+        per1 = L1 // P
+        pools1 = [(torch.randn((per1, K1, P, D), device="cuda"), torch.randn((per1, K1, P, D), device="cuda"))
+                  for _ in range(copies)]
+        bt1 = (torch.randperm(per1, generator=gen) + 1).to(torch.int32).cuda()
+        q1 = torch.randn((1, H1, D), device="cuda")
+        o1 = torch.empty_like(q1)
+        pos1 = torch.tensor([L1 - 1], dtype=torch.int32, device="cuda")
+        be = ti.HipBackend()
+        ws1 = ti.attention_workspace(be, q1, pools1[0][0])
+        ms1 = time_graph(lambda i: ti.attention_(be, o1, ws1, q1, pools1[i % copies][0], pools1[i % copies][1],
+                                                 bt1, pos1, scale))
+        b1 = 2 * L1 * K1 * D * 4 + 2 * H1 * D * 4
+        extra["decode_fp32_qwen3_06b_ctx1024"] = {"us": round(ms1 * 1e3, 2), "GB/s": round(b1 / ms1 / 1e6, 1)}
+        del pools1
     if want("verify"):
         sv = decode_setup(16, 4096 + 16, 16, 32, 8, D, P, 2, gen)
         msv = time_graph(lambda i: decode_call(sv, i, scale))

@@ -76,6 +76,7 @@ int ti_attention_workspace_bytes(const ti_attention_args *a, const ti_kv_cache *
     if (st) return st;
     const int path = resolve_path(a, c);
     if (path < 0) return -path;
+    if (path == 0) ti_plan_generic(a, c, bytes);
     if (path == 1) *bytes = ti_plan_decode(a, c).bytes;
     if (path == 2) *bytes = ti_plan_prefill(a, c, false).bytes;
     return TI_OK;

@@ -136,4 +136,6 @@ struct ti_prefill_plan {
 ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c, bool bound_keys);
 int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti_prefill_plan &p,
                       hipStream_t s);
+// fp32 path: its key splits and workspace bytes (host shapes only).
+int ti_plan_generic(const ti_attention_args *a, const ti_kv_cache *c, size_t *bytes);
 int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s);

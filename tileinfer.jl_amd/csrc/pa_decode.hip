@@ -10,7 +10,7 @@ namespace {
 // Merge the splits of packed rows: grid (ceil(M / 4), Hk, B), four waves, one row per
 // wave; lane owns head-dim elements lane + 64 k. The running maxima and sums are
 // wave-uniform loads; the partial rows are read coalesced, with no LDS and no barrier.
-template <int D>
+template <int D, typename T>
 __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     constexpr int PER = D / 64;
     const int lane = threadIdx.x & 63;
@@ -57,9 +57,9 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
         }
     }
     const float inv = 1.0f / lsum;
-    uint16_t *o = p.out + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
+    T *o = reinterpret_cast<T *>(p.out) + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
 #pragma unroll
-    for (int k = 0; k < PER; k++) o[lane + 64 * k] = f2bf(acc[k] * inv);
+    for (int k = 0; k < PER; k++) Elt<T>::st(o, lane + 64 * k, acc[k] * inv);
 }
 
 template <int D, bool INT8, bool PG16, int NW>
@@ -182,7 +182,13 @@ int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows
     p.M = rows;
     p.splits = splits;
     dim3 cgrid((rows + 3) / 4, c->kv_heads, a->num_seqs);
-    if (c->head_dim == 128) combine_kernel<128><<<cgrid, 256, 0, s>>>(p);
-    else combine_kernel<64><<<cgrid, 256, 0, s>>>(p);
+    const bool f32 = a->dtype == TI_F32;
+    if (c->head_dim == 128) {
+        if (f32) combine_kernel<128, float><<<cgrid, 256, 0, s>>>(p);
+        else combine_kernel<128, uint16_t><<<cgrid, 256, 0, s>>>(p);
+    } else {
+        if (f32) combine_kernel<64, float><<<cgrid, 256, 0, s>>>(p);
+        else combine_kernel<64, uint16_t><<<cgrid, 256, 0, s>>>(p);
+    }
     return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
 }

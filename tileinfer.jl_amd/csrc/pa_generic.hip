@@ -3,9 +3,12 @@
 // operands to bf16 for the matrix cores. It also accepts bf16 and INT8 caches, which makes
 // it an independent cross-check of the MFMA kernels. Probabilities stay in Float32.
 //
-// Grid (max_query_len, Hq, B), one wave per (query token, query head): the keys of the
-// step are walked 64 at a time, lane = key for QK^T (a full dot product per lane), then
-// lane = head-dim element for PV with the probabilities broadcast through LDS.
+// Grid (max_query_len x splits, Hq, B), one wave per (query token, query head, key split):
+// the split's keys are walked 64 at a time, lane = key for QK^T (a full dot product per
+// lane), then lane = head-dim element for PV with the probabilities broadcast through LDS.
+// With one split the wave writes the output row; otherwise it writes a Float32 partial
+// (acc[D], m, l) in the decode kernel's layout (packed row g + G t of its KV head) and the
+// combine kernel merges the splits.
 // Semantics as attention(::RefBackend) (src/ops/reference.jl:95-121): key i visible to
 // query t iff i <= start + t (causal) or i < start + n (not causal).
 #include "common.hpp"
@@ -21,19 +24,24 @@ struct GenericParams {
     const int8_t *lq;
     const float *ls, *smooth;
     const int32_t *positions, *qsl, *bt;
-    int bt_stride, num_pages, P, Hk, Hq, G, nmax, causal;
+    float *part;                 // split partials [B][Hk][splits][G nmax][D + 2]
+    int bt_stride, num_pages, P, Hk, Hq, G, nmax, causal, splits;
     float scale_log2;
 };
 
 template <typename T, bool INT8, int D>
 __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) {
     using E = Elt<T>;
-    const int t = blockIdx.x, hq = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
+    const int t = blockIdx.x / p.splits, split = blockIdx.x % p.splits;
+    const int hq = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
     const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
     if (t >= nb) return;
     const int start = p.positions[tok0], len = start + nb;
     const int last = p.causal ? start + t : len - 1;
+    // this split's keys: [k0, k1) of the sequence's len, cut at the query's last key
+    const int per = (len + p.splits - 1) / p.splits;
+    const int k0 = split * per, k1 = min(k0 + per, last + 1);
     const int g = hq / p.G;
     const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
     const size_t half_q = (size_t)p.num_pages * p.Hk * p.P * D;
@@ -51,9 +59,9 @@ __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) 
 #pragma unroll
     for (int j = 0; j < PER; j++) acc[j] = 0.0f;
     float m = NEG_BIG, l = 0.0f;
-    for (int c0 = 0; c0 <= last; c0 += WAVE) {
+    for (int c0 = k0; c0 < k1; c0 += WAVE) {
         const int key = c0 + lane;
-        const bool valid = key <= last;
+        const bool valid = key < k1;
         float s = -INFINITY;
         long long row = 0;
         if (valid) {
@@ -78,7 +86,7 @@ __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) 
         ps[lane] = pr;
         rows[lane] = row;
         __syncthreads();
-        const int cnt = min(WAVE, last + 1 - c0);
+        const int cnt = min(WAVE, k1 - c0);
 #pragma unroll
         for (int j = 0; j < PER; j++) acc[j] *= alpha;
         for (int kk = 0; kk < cnt; kk++) {
@@ -96,6 +104,22 @@ __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) 
         }
         __syncthreads();
     }
+    if (p.splits > 1) {
+        // (acc, m, l) of packed row (hq mod G) + G t of KV head g; a split without keys
+        // leaves m = NEG_BIG, l = 0, acc = 0, which the combine weights to zero.
+        const int M = p.G * p.nmax, r = (hq - g * p.G) + p.G * t;
+        float *dst = p.part + ((((size_t)b * p.Hk + g) * p.splits + split) * M + r) * (D + 2);
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const int d = lane + WAVE * j;
+            if (d < D) dst[d] = acc[j];
+        }
+        if (lane == 0) {
+            dst[D] = m;
+            dst[D + 1] = l;
+        }
+        return;
+    }
     T *o = (T *)p.out + ((size_t)(tok0 + t) * p.Hq + hq) * D;
 #pragma unroll
     for (int j = 0; j < PER; j++) {
@@ -111,6 +135,17 @@ void launch(const GenericParams &p, int D, dim3 grid, hipStream_t s) {
 }
 
 }  // namespace
+
+// Key splits for the fp32 path: while the waves (tokens x query heads x sequences) are
+// fewer than about 1024, double the splits (at most 32). Host shapes only (graph-safe).
+int ti_plan_generic(const ti_attention_args *a, const ti_kv_cache *c, size_t *bytes) {
+    const long long waves = (long long)a->max_query_len * a->q_heads * a->num_seqs;
+    int sp = 1;
+    while (sp < 32 && waves * sp < 1024) sp <<= 1;
+    const int rows = a->q_heads / c->kv_heads * a->max_query_len;
+    *bytes = sp == 1 ? 0 : (size_t)a->num_seqs * c->kv_heads * sp * rows * (c->head_dim + 2) * sizeof(float);
+    return sp;
+}
 
 int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s) {
     GenericParams p;
@@ -133,7 +168,11 @@ int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStrea
     p.nmax = a->max_query_len;
     p.causal = a->causal;
     p.scale_log2 = a->scale * LOG2E;
-    dim3 grid(a->max_query_len, a->q_heads, a->num_seqs);
+    size_t bytes = 0;
+    p.splits = ti_plan_generic(a, c, &bytes);
+    if (bytes > 0 && (!a->workspace || a->workspace_bytes < bytes)) p.splits = 1;   // runs unsplit
+    p.part = (float *)a->workspace;
+    dim3 grid(a->max_query_len * p.splits, a->q_heads, a->num_seqs);
     const bool int8 = c->kind == TI_KV_INT8;
     if (a->dtype == TI_BF16) {
         if (int8) launch<uint16_t, true>(p, c->head_dim, grid, s);
@@ -142,5 +181,7 @@ int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStrea
         if (int8) launch<float, true>(p, c->head_dim, grid, s);
         else launch<float, false>(p, c->head_dim, grid, s);
     }
-    return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
+    if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
+    return p.splits > 1 ? ti_launch_combine(a, c, a->q_heads / c->kv_heads * a->max_query_len, p.splits, s)
+                        : TI_OK;
 }
