@@ -104,6 +104,15 @@ def test_unsupported_shapes_and_workspace():
     assert L.ti_attention(ctypes.byref(_args()), ctypes.byref(_cache()), None) == _lib.TI_ERR_WORKSPACE
     a = _args(workspace=0x1000, workspace_bytes=10)
     assert L.ti_attention(ctypes.byref(a), ctypes.byref(_cache()), None) == _lib.TI_ERR_WORKSPACE
+    # sequences and prefill q-tiles live in grid dimensions of at most 65535
+    a = _args(num_seqs=70000, total_tokens=70000)
+    assert L.ti_attention(ctypes.byref(a), ctypes.byref(_cache()), None) == _lib.TI_ERR_UNSUPPORTED
+    assert ws(a, _cache())[0] == _lib.TI_ERR_UNSUPPORTED
+    # G = 64 packs two queries per four-wave q-tile: 140000 tokens are 70000 tiles
+    a = _args(q_heads=64, num_seqs=1, max_query_len=140000, total_tokens=140000)
+    c = _cache(kv_heads=1)
+    assert ws(a, c)[0] == _lib.TI_ERR_UNSUPPORTED
+    assert L.ti_attention(ctypes.byref(a), ctypes.byref(c), None) == _lib.TI_ERR_UNSUPPORTED
 
 
 def test_store_rope_inputs_validation():

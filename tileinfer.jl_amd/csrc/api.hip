@@ -4,7 +4,7 @@
 
 namespace {
 
-bool bad_cache(const ti_kv_cache *c, bool need_attention_dims) {
+bool bad_cache(const ti_kv_cache *c) {
     if (!c) return true;
     if (c->kind != TI_KV_DENSE && c->kind != TI_KV_INT8) return true;
     if (c->head_dim <= 0 || (c->head_dim & 1) || c->page_size <= 0 || c->kv_heads <= 0 ||
@@ -12,7 +12,6 @@ bool bad_cache(const ti_kv_cache *c, bool need_attention_dims) {
         return true;
     if (c->kind == TI_KV_DENSE && (!c->k_pages || !c->v_pages)) return true;
     if (c->kind == TI_KV_INT8 && (!c->layer_q || !c->layer_scale || !c->smooth)) return true;
-    (void)need_attention_dims;
     return false;
 }
 
@@ -38,7 +37,7 @@ int resolve_path(const ti_attention_args *a, const ti_kv_cache *c) {
 }
 
 int check_attention(const ti_attention_args *a, const ti_kv_cache *c) {
-    if (!a || bad_cache(c, true) || bad_dtype(a->dtype)) return TI_ERR_INVALID_ARG;
+    if (!a || bad_cache(c) || bad_dtype(a->dtype)) return TI_ERR_INVALID_ARG;
     if (c->head_dim != 64 && c->head_dim != 128) return TI_ERR_UNSUPPORTED;
     if (a->q_heads <= 0 || a->q_heads % c->kv_heads) return TI_ERR_INVALID_ARG;
     if (a->num_seqs <= 0 || a->max_query_len <= 0 || a->total_tokens <= 0 ||
@@ -49,6 +48,8 @@ int check_attention(const ti_attention_args *a, const ti_kv_cache *c) {
         return TI_ERR_INVALID_ARG;
     if (a->causal != 0 && a->causal != 1) return TI_ERR_INVALID_ARG;
     if (!(a->scale == a->scale)) return TI_ERR_INVALID_ARG;
+    // launch grids put sequences in a dimension of at most 65535
+    if (a->num_seqs > 65535) return TI_ERR_UNSUPPORTED;
     return TI_OK;
 }
 
@@ -78,7 +79,11 @@ int ti_attention_workspace_bytes(const ti_attention_args *a, const ti_kv_cache *
     if (path < 0) return -path;
     if (path == 0) ti_plan_generic(a, c, bytes);
     if (path == 1) *bytes = ti_plan_decode(a, c).bytes;
-    if (path == 2) *bytes = ti_plan_prefill(a, c, false).bytes;
+    if (path == 2) {
+        const ti_prefill_plan pp = ti_plan_prefill(a, c, false);
+        if (pp.qtiles > 65535) return TI_ERR_UNSUPPORTED;
+        *bytes = (long long)pp.qtiles * pp.splits > 65535 ? 0 : pp.bytes;
+    }
     return TI_OK;
 }
 
@@ -93,6 +98,8 @@ int ti_attention(const ti_attention_args *a, const ti_kv_cache *c, void *stream)
         // The prefill path never requires a workspace (the reference runs its prefill
         // kernel exactly when none is passed); without one it runs unsplit.
         ti_prefill_plan pp = ti_plan_prefill(a, c, true);
+        if ((long long)pp.qtiles * pp.splits > 65535) pp.splits = 1;
+        if (pp.qtiles > 65535) return TI_ERR_UNSUPPORTED;   // q-tiles share grid y (at most 65535)
         if (pp.bytes > 0 && (!a->workspace || a->workspace_bytes < pp.bytes)) {
             pp.splits = 1;
             pp.bytes = 0;
@@ -106,7 +113,7 @@ int ti_attention(const ti_attention_args *a, const ti_kv_cache *c, void *stream)
 
 int ti_store_kv(int dtype, const ti_kv_cache *c, const void *k, const void *v,
                 const int32_t *slots, int n, void *stream) {
-    if (bad_dtype(dtype) || bad_cache(c, false) || n < 0) return TI_ERR_INVALID_ARG;
+    if (bad_dtype(dtype) || bad_cache(c) || n < 0) return TI_ERR_INVALID_ARG;
     if (c->head_dim > 512) return TI_ERR_UNSUPPORTED;
     if (n == 0) return TI_OK;
     if (!k || !v || !slots) return TI_ERR_INVALID_ARG;
@@ -137,7 +144,7 @@ int ti_attention_inputs(int dtype, void *q_out, const ti_kv_cache *c, const void
                         const void *q_norm, const void *k_norm, const void *cos_sin,
                         int table_len, const int32_t *positions, const int32_t *slots, int n,
                         int q_heads, float eps, void *stream) {
-    if (bad_dtype(dtype) || bad_cache(c, false) || n < 0 || q_heads <= 0 || table_len <= 0)
+    if (bad_dtype(dtype) || bad_cache(c) || n < 0 || q_heads <= 0 || table_len <= 0)
         return TI_ERR_INVALID_ARG;
     if (c->head_dim > 128) return TI_ERR_UNSUPPORTED;
     if ((q_norm == nullptr) != (k_norm == nullptr)) return TI_ERR_INVALID_ARG;

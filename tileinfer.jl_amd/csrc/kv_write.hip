@@ -29,8 +29,8 @@ __global__ void __launch_bounds__(256) rope_kernel(T *__restrict__ y, const T *_
                                                    const int32_t *__restrict__ positions,
                                                    int heads, int D) {
     using E = Elt<T>;
-    const int t = blockIdx.y, half = D / 2;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const int t = blockIdx.x, half = D / 2;   // tokens on x: no 65535 limit
+    const int idx = blockIdx.y * blockDim.x + threadIdx.x;
     if (idx >= heads * half) return;
     const int p = positions[t];
     if (p < 0 || p >= table_len) return;
@@ -263,7 +263,7 @@ int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows
 int ti_launch_rope(int dtype, void *y, const void *x, const void *cos_t, const void *sin_t,
                    int table_len, const int32_t *positions, int n, int heads, int D,
                    hipStream_t s) {
-    dim3 grid((heads * (D / 2) + 255) / 256, n);
+    dim3 grid(n, (heads * (D / 2) + 255) / 256);
     if (dtype == TI_BF16)
         rope_kernel<uint16_t><<<grid, 256, 0, s>>>((uint16_t *)y, (const uint16_t *)x,
                                                    (const uint16_t *)cos_t, (const uint16_t *)sin_t,
