@@ -108,11 +108,24 @@ def test_unsupported_shapes_and_workspace():
     a = _args(num_seqs=70000, total_tokens=70000)
     assert L.ti_attention(ctypes.byref(a), ctypes.byref(_cache()), None) == _lib.TI_ERR_UNSUPPORTED
     assert ws(a, _cache())[0] == _lib.TI_ERR_UNSUPPORTED
-    # G = 64 packs two queries per four-wave q-tile: 140000 tokens are 70000 tiles
-    a = _args(q_heads=64, num_seqs=1, max_query_len=140000, total_tokens=140000)
+    # G = 64 packs two queries per four-wave q-tile: 140000 tokens are 70000 tiles; the
+    # 8-wave kernel packs four (35000 tiles, supported), so 300000 tokens exceed both
     c = _cache(kv_heads=1)
+    a = _args(q_heads=64, num_seqs=1, max_query_len=300000, total_tokens=300000)
     assert ws(a, c)[0] == _lib.TI_ERR_UNSUPPORTED
     assert L.ti_attention(ctypes.byref(a), ctypes.byref(c), None) == _lib.TI_ERR_UNSUPPORTED
+    a = _args(q_heads=64, num_seqs=1, max_query_len=140000, total_tokens=140000)
+    assert ws(a, c)[0] == _lib.TI_OK
+    old = os.environ.get("TI_PREFILL_PP")
+    os.environ["TI_PREFILL_PP"] = "0"
+    try:
+        assert ws(a, c)[0] == _lib.TI_ERR_UNSUPPORTED
+        assert L.ti_attention(ctypes.byref(a), ctypes.byref(c), None) == _lib.TI_ERR_UNSUPPORTED
+    finally:
+        if old is None:
+            del os.environ["TI_PREFILL_PP"]
+        else:
+            os.environ["TI_PREFILL_PP"] = old
 
 
 def test_store_rope_inputs_validation():

@@ -68,9 +68,24 @@ def test_random_shape(gpu, seed):
             paths.append(ti.TI_PATH_DECODE)
         paths.append(ti.TI_PATH_PREFILL)
     tol = 1e-4 if kind == "fp32" else 2e-2
-    for path in paths:
-        out = torch.full_like(qd, float("nan"))
-        ws = ti.attention_workspace(BE, qd, k, path=path)
-        ti.attention_(BE, out, ws, qd, k, v, btd, pos, scale, causal, path=path)
+    runs = [(path, None) for path in paths]
+    if kind == "bf16":
+        # the prefill path through both prefill kernels (TI_PREFILL_PP=1 takes the 8-wave
+        # ping-pong kernel wherever its shape limits allow, =0 never)
+        runs += [(ti.TI_PATH_PREFILL, "1"), (ti.TI_PATH_PREFILL, "0")]
+    for path, pp in runs:
+        old = os.environ.get("TI_PREFILL_PP")
+        if pp is not None:
+            os.environ["TI_PREFILL_PP"] = pp
+        try:
+            out = torch.full_like(qd, float("nan"))
+            ws = ti.attention_workspace(BE, qd, k, path=path)
+            ti.attention_(BE, out, ws, qd, k, v, btd, pos, scale, causal, path=path)
+        finally:
+            if pp is not None:
+                if old is None:
+                    del os.environ["TI_PREFILL_PP"]
+                else:
+                    os.environ["TI_PREFILL_PP"] = old
         err = float(np.max(np.abs(ref - out.float().cpu().numpy())))
-        assert err <= tol, f"path {path}: max abs err {err}"
+        assert err <= tol, f"path {path} pp {pp}: max abs err {err}"

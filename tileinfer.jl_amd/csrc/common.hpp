@@ -123,6 +123,7 @@ int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows
                       hipStream_t s);
 
 struct ti_prefill_plan {
+    int pp;          // 1: the 8-wave ping-pong kernel (pa_prefill_pp.hip)
     int wpg;         // waves per key group (32 packed rows each)
     int ng;          // key groups per work-group
     int splits;      // key splits across work-groups (partials merged by the combine kernel)
@@ -136,6 +137,9 @@ struct ti_prefill_plan {
 ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c, bool bound_keys);
 int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti_prefill_plan &p,
                       hipStream_t s);
+bool ti_prefill_pp_eligible(const ti_attention_args *a, const ti_kv_cache *c);
+int ti_launch_prefill_pp(const ti_attention_args *a, const ti_kv_cache *c, const ti_prefill_plan &p,
+                         hipStream_t s);
 // fp32 path: its key splits and workspace bytes (host shapes only).
 int ti_plan_generic(const ti_attention_args *a, const ti_kv_cache *c, size_t *bytes);
 int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s);

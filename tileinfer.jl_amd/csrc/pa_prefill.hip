@@ -577,6 +577,34 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     ti_prefill_plan pl;
     const int G = a->q_heads / c->kv_heads;
     const long long pairs = (long long)c->kv_heads * a->num_seqs;
+    const long long key_tiles = ((long long)a->block_table_stride * c->page_size + 31) / 32;
+    // The 8-wave ping-pong kernel (256 packed rows per work-group, one per CU) is taken
+    // when its work-groups fill the 256 CUs at least twice without key splits: measured
+    // 906 vs 745 TFLOP/s at a 4096-token causal prefill (512 work-groups), but slower
+    // at 2048 tokens (256) and below, where the four-wave kernel's smaller q-tiles and
+    // in-work-group key groups keep more CUs busy. TI_PREFILL_PP=1 takes it whenever the
+    // shapes allow, TI_PREFILL_PP=0 never (tuning and tests; read per call).
+    const char *pp_env = getenv("TI_PREFILL_PP");
+    const int pp_force = pp_env ? atoi(pp_env) : -1;
+    const long long pp_wgs = (long long)((a->max_query_len + 256 / G - 1) / (256 / G)) * pairs;
+    pl.pp = ti_prefill_pp_eligible(a, c) && (pp_force == 1 || (pp_force != 0 && pp_wgs >= 512));
+    if (pl.pp) {
+        // Key splits (forced runs on small grids) while work-groups are fewer than the
+        // CUs and every split keeps at least 8 key tiles of the longest context the
+        // block tables can hold.
+        pl.wpg = 8;
+        pl.ng = 1;
+        pl.TQ = 256 / G;
+        pl.qtiles = (a->max_query_len + pl.TQ - 1) / pl.TQ;
+        const long long wgs = (long long)pl.qtiles * pairs;
+        pl.splits = 1;
+        while (pl.splits < 16 && wgs * pl.splits < 256 && (!bound_keys || key_tiles / (2 * pl.splits) >= 8))
+            pl.splits *= 2;
+        if (forced_splits >= 1 && forced_splits <= 64) pl.splits = forced_splits;
+        pl.rows = G * a->max_query_len;
+        pl.bytes = pl.splits == 1 ? 0 : (size_t)pairs * pl.splits * pl.rows * (c->head_dim + 2) * sizeof(float);
+        return pl;
+    }
     pl.wpg = (long long)((a->max_query_len + 128 / G - 1) / (128 / G)) * pairs >= 256 ? 4 : 2;
     if (forced_wpg == 2 || forced_wpg == 4) pl.wpg = forced_wpg;
     if (32 * pl.wpg < G) pl.wpg = 4;
@@ -588,7 +616,6 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     if (pl.wpg == 4 && pl.ng > 2) pl.ng = 2;   // 16 waves of this kernel do not fit one CU's registers
     // Split the keys while work-groups are fewer than the CUs and every split keeps at
     // least 4 steps per key group of the longest context the block tables can hold.
-    const long long key_tiles = ((long long)a->block_table_stride * c->page_size + 31) / 32;
     pl.splits = 1;
     while (pl.splits < 16 && wgs * pl.splits < 256 &&
            (!bound_keys || key_tiles / (2 * pl.splits) >= 4LL * pl.ng))
@@ -601,6 +628,7 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
 
 int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti_prefill_plan &pl,
                       hipStream_t s) {
+    if (pl.pp) return ti_launch_prefill_pp(a, c, pl, s);
     PrefillParams p;
     p.q = (const uint16_t *)a->q;
     p.out = (uint16_t *)a->out;
