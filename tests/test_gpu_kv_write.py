@@ -204,3 +204,36 @@ def test_out_of_range_slots_are_skipped(gpu):
     torch.cuda.synchronize()
     assert kp.sum().item() == H * D                     # only slot 2 was written
     assert kp[0, :, 1].float().eq(1).all()
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_inputs_out_of_range(gpu, D):
+    """Tokens whose slot lies outside the pool write no K/V row, tokens whose position
+    lies outside the rotary table write nothing (the q rows keep what they held); every
+    other token is written as the oracle writes it. D = 128 runs the 16-lanes-per-head
+    kernel, D = 64 the one-wave-per-head kernel."""
+    nq, nkv, P, pages, L = 4, 2, 4, 3, 32
+    g = rng(700 + D)
+    positions = np.array([3, 5, 40, 7], np.int32)            # 40 is past the table
+    slots = np.array([2, 13, 5, 0], np.int32)                # 13 and 0 are outside the pool
+    n = len(positions)
+    c, s, table = _table(g, D, L, True)
+    qkv = randn(g, n, nq + 2 * nkv, D, bf16=True)
+    q = torch.full((n, nq, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    kp = torch.zeros((pages, nkv, P, D), dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    ti.attention_inputs_(BE, q, kp, vp, dev(qkv, True), None, None, table,
+                         torch.from_numpy(positions).cuda(), torch.from_numpy(slots).cuda(), 1e-6)
+    keep = np.array([0, 1, 3])                               # tokens with an in-table position
+    cs_tab = np.stack([c, s], 1)
+    scratch = [np.zeros((pages, nkv, P, D), np.float32) for _ in range(2)]
+    rq = orc.attention_inputs(qkv[keep], None, None, cs_tab, positions[keep], np.ones(3, np.int32),
+                              nq, nkv, 1e-6, True, k_pages=scratch[0], v_pages=scratch[1])
+    # only token 0 has both an in-table position and an in-pool slot
+    rkp, rvp = np.zeros((pages, nkv, P, D), np.float32), np.zeros((pages, nkv, P, D), np.float32)
+    orc.attention_inputs(qkv[:1], None, None, cs_tab, positions[:1], slots[:1], nq, nkv, 1e-6, True,
+                         k_pages=rkp, v_pages=rvp)
+    got_q = host(q)
+    assert np.array_equal(got_q[keep], rq)
+    assert (got_q[2] == 7.0).all()
+    assert np.array_equal(host(kp), rkp) and np.array_equal(host(vp), rvp)

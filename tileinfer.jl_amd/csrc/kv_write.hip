@@ -249,6 +249,106 @@ __global__ void __launch_bounds__(64) attention_inputs_kernel(
     }
 }
 
+// Vectorized form of attention_inputs_kernel for dense caches with head_dim 128: 16 lanes
+// per head, lane u owning elements 4u .. 4u + 3 of each half (8-byte bf16 / 16-byte
+// Float32 loads), 16 heads per 256-thread work-group: grid (n, ceil((nq + nkv) / 16)).
+// Same rounding points element by element. With the q/k norm, each lane keeps the four
+// per-lane partials a_i^2 + b_i^2 (i = 4u + e) that the one-wave kernel's lanes hold and
+// combines them in that kernel's butterfly order (xor 32, 16, 8, 4 across lanes u ^ 8,
+// u ^ 4, u ^ 2, u ^ 1, then xor 2 and 1 inside the lane), so the sum of squares, and with
+// it every output, is bit-identical to the one-wave kernel and to rmsnorm_kernel.
+template <typename T> struct Vec4;
+template <> struct Vec4<uint16_t> {
+    static __device__ __forceinline__ void ld(const uint16_t *p, float (&x)[4]) {
+        const uint2 w = *reinterpret_cast<const uint2 *>(p);
+        x[0] = __uint_as_float(w.x << 16);
+        x[1] = __uint_as_float(w.x & 0xffff0000u);
+        x[2] = __uint_as_float(w.y << 16);
+        x[3] = __uint_as_float(w.y & 0xffff0000u);
+    }
+    static __device__ __forceinline__ void st(uint16_t *p, const float (&x)[4]) {
+        const uint2 w = make_uint2((uint32_t)f2bf(x[0]) | ((uint32_t)f2bf(x[1]) << 16),
+                                   (uint32_t)f2bf(x[2]) | ((uint32_t)f2bf(x[3]) << 16));
+        *reinterpret_cast<uint2 *>(p) = w;
+    }
+};
+template <> struct Vec4<float> {
+    static __device__ __forceinline__ void ld(const float *p, float (&x)[4]) {
+        const float4 w = *reinterpret_cast<const float4 *>(p);
+        x[0] = w.x; x[1] = w.y; x[2] = w.z; x[3] = w.w;
+    }
+    static __device__ __forceinline__ void st(float *p, const float (&x)[4]) {
+        *reinterpret_cast<float4 *>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    }
+};
+
+template <typename T, bool NORM>
+__global__ void __launch_bounds__(256) attention_inputs_v_kernel(
+    T *__restrict__ q_out, T *__restrict__ kp, T *__restrict__ vp, const T *__restrict__ qkv,
+    const T *__restrict__ q_norm, const T *__restrict__ k_norm, const T *__restrict__ cos_sin,
+    int table_len, const int32_t *__restrict__ positions, const int32_t *__restrict__ slots,
+    int nq, int nkv, int P, int pages, float eps) {
+    constexpr int D = 128, HALF = 64;
+    using E = Elt<T>;
+    using V = Vec4<T>;
+    const int t = blockIdx.x, j = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
+    if (j >= nq + nkv) return;   // a whole 16-lane group
+    const int pos = positions[t];
+    if (pos < 0 || pos >= table_len) return;
+    const bool is_q = j < nq;
+    const int h = j - nq;
+    long long row = 0;
+    if (!is_q) {
+        row = slot_row(slots[t], h, P, nkv, pages);
+        if (row < 0) return;
+    }
+    const size_t col = ((size_t)t * (nq + 2 * nkv) + j) * D;
+    float a[4], b[4];
+    V::ld(qkv + col + 4 * u, a);
+    V::ld(qkv + col + HALF + 4 * u, b);
+    if (NORM) {
+        float pp[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) pp[e] = a[e] * a[e] + b[e] * b[e];
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1)
+#pragma unroll
+            for (int e = 0; e < 4; e++) pp[e] = pp[e] + __shfl_xor(pp[e], o);
+        const float p02 = pp[0] + pp[2], p13 = pp[1] + pp[3];
+        const float ss = p02 + p13;
+        const float inv_rms = __frcp_rn(__fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+        const T *wn = is_q ? q_norm : k_norm;
+        float w1[4], w2[4];
+        V::ld(wn + 4 * u, w1);
+        V::ld(wn + HALF + 4 * u, w2);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            a[e] = E::rnd(E::rnd(a[e] * inv_rms) * w1[e]);
+            b[e] = E::rnd(E::rnd(b[e] * inv_rms) * w2[e]);
+        }
+    }
+    const T *cs = cos_sin + (size_t)pos * 2 * D;
+    float c1[4], c2[4], s1[4], s2[4], y1[4], y2[4];
+    V::ld(cs + 4 * u, c1);
+    V::ld(cs + HALF + 4 * u, c2);
+    V::ld(cs + D + 4 * u, s1);
+    V::ld(cs + D + HALF + 4 * u, s2);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        y1[e] = E::rnd(E::rnd(a[e] * c1[e]) + E::rnd(-b[e] * s1[e]));
+        y2[e] = E::rnd(E::rnd(b[e] * c2[e]) + E::rnd(a[e] * s2[e]));
+    }
+    T *dst = is_q ? q_out + ((size_t)t * nq + j) * D : kp + (size_t)row * D;
+    V::st(dst + 4 * u, y1);
+    V::st(dst + HALF + 4 * u, y2);
+    if (is_q) return;
+    // the value row: a bit copy, D * sizeof(T) bytes in 16-byte chunks over the 16 lanes
+    const uint4 *vs = reinterpret_cast<const uint4 *>(qkv + ((size_t)t * (nq + 2 * nkv) + nq + nkv + h) * D);
+    uint4 *vd = reinterpret_cast<uint4 *>(vp + (size_t)row * D);
+#pragma unroll
+    for (int c = u; c < D * (int)sizeof(T) / 16; c += 16) vd[c] = vs[c];
+}
+
 }  // namespace
 
 int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int H, float eps,
@@ -304,6 +404,14 @@ static void launch_inputs(void *q_out, const ti_kv_cache *c, const void *qkv, co
                           const void *k_norm, const void *cos_sin, int table_len,
                           const int32_t *positions, const int32_t *slots, int n, int nq,
                           float eps, hipStream_t s) {
+    if (!INT8 && c->head_dim == 128) {
+        dim3 grid(n, (nq + c->kv_heads + 15) / 16);
+        attention_inputs_v_kernel<T, NORM><<<grid, 256, 0, s>>>(
+            (T *)q_out, (T *)c->k_pages, (T *)c->v_pages, (const T *)qkv, (const T *)q_norm,
+            (const T *)k_norm, (const T *)cos_sin, table_len, positions, slots, nq, c->kv_heads,
+            c->page_size, c->num_pages, eps);
+        return;
+    }
     dim3 grid(n, nq + c->kv_heads);
     attention_inputs_kernel<T, NORM, INT8><<<grid, 64, 0, s>>>(
         (T *)q_out, (T *)c->k_pages, (T *)c->v_pages, c->layer_q, c->layer_scale, c->smooth,
