@@ -346,20 +346,22 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         f32x16 sc, sc2;
 #pragma unroll
         for (int e = 0; e < 16; e++) sc[e] = sc2[e] = 0.0f;
+        // All K reads go out before the first score MFMA (one LDS latency per tile instead
+        // of one per MFMA pair); the next tile's global loads are spread between the MFMAs
+        // so the CU's load path drains while the matrix cores run.
         const uint16_t *krow = &sm.k[buf][r32 * Smem<D>::KROW + kg * 8];
+        u32x4 ka[NQB];
+#pragma unroll
+        for (int i = 0; i < NQB; i++) ka[i] = *reinterpret_cast<const u32x4 *>(krow + i * 16);
 #pragma unroll
         for (int i = 0; i < NQB; i += 2) {
-            const bf16x8 a0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + i * 16));
-            const bf16x8 a1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + (i + 1) * 16));
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qreg[i], sc, 0, 0, 0);
-            sc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qreg[i + 1], sc2, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka[i]), qreg[i], sc, 0, 0, 0);
+            sc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka[i + 1]), qreg[i + 1], sc2, 0, 0, 0);
         }
-        // Spread the next tile's global loads between the score MFMAs and their K reads,
-        // so the CU's load path drains while the matrix cores run.
+        __builtin_amdgcn_sched_group_barrier(0x0100, NQB, 0);   // all K reads
 #pragma unroll
         for (int i = 0; i < NQB; i++) {
             __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);   // one global load
-            __builtin_amdgcn_sched_group_barrier(0x0100, 1, 0);   // one LDS read
             __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);   // one MFMA
         }
         sc += sc2;
