@@ -53,7 +53,11 @@ def test_decode_step_graph_replays_as_sequences_grow(gpu, B, n):
         assert torch.equal(got, ref), f"replay {step} differs from eager"
 
 
-def test_prefill_and_kv_write_graph(gpu):
+@pytest.mark.parametrize("pp", [None, "1"])
+def test_prefill_and_kv_write_graph(gpu, pp, monkeypatch):
+    """pp = "1": the 8-wave ping-pong prefill kernel (TI_PREFILL_PP=1), else AUTO's choice."""
+    if pp is not None:
+        monkeypatch.setenv("TI_PREFILL_PP", pp)
     Hq, Hk, D, P, n = 32, 8, 128, 16, 128
     torch.manual_seed(7)
     pages = 64
