@@ -218,10 +218,18 @@ __device__ __forceinline__ void store_tile(const Stage<D, INT8, GT> &st, Smem<D>
         const int c = gtid + GT * u, key = c / CPR, ch = c % CPR;
         if (c < Stage<D, INT8, GT>::CH) {
             const u32x4 kv = INT8 ? i8x8_to_bf16x8(st.k[u][0], st.k[u][1]) : st.k[u];
-            u32x4 vv = INT8 ? i8x8_to_bf16x8(st.v[u][0], st.v[u][1]) : st.v[u];
-            if (partial && key >= valid_keys) vv = (u32x4){0u, 0u, 0u, 0u};   // p = 0 meets 0
+            const u32x4 vv = INT8 ? i8x8_to_bf16x8(st.v[u][0], st.v[u][1]) : st.v[u];
             *reinterpret_cast<u32x4 *>(&sm.k[buf][key * Smem<D>::KROW + ch * 8]) = kv;
-            *reinterpret_cast<u32x4 *>(&sm.v[buf][key * Smem<D>::VROW + ch * 8]) = vv;
+            if (partial) {
+                // Only the last tile has keys past the step's end (their values meet p = 0 and
+                // must be finite); the empty asm keeps this a real branch, so full tiles skip
+                // the selects.
+                asm volatile("");
+                const uint32_t keep = key < valid_keys ? ~0u : 0u;
+                *reinterpret_cast<u32x4 *>(&sm.v[buf][key * Smem<D>::VROW + ch * 8]) = vv & keep;
+            } else {
+                *reinterpret_cast<u32x4 *>(&sm.v[buf][key * Smem<D>::VROW + ch * 8]) = vv;
+            }
         }
     }
     if (INT8 && gtid < 2 * KT) {
@@ -341,11 +349,11 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
 
     auto compute = [&](int kt, int buf, auto &&issue_loads) {
         issue_loads();
-        // Two independent accumulation chains (even / odd head-dim blocks) halve the
-        // dependent-MFMA latency of the score tile.
-        f32x16 sc, sc2;
+        // One accumulation chain: dependent v_mfma_f32_32x32x16_bf16 issue back to back
+        // (31 cycles each, measured), and a second chain would cost 16 VALU adds.
+        f32x16 sc;
 #pragma unroll
-        for (int e = 0; e < 16; e++) sc[e] = sc2[e] = 0.0f;
+        for (int e = 0; e < 16; e++) sc[e] = 0.0f;
         // All K reads go out before the first score MFMA (one LDS latency per tile instead
         // of one per MFMA pair); the next tile's global loads are spread between the MFMAs
         // so the CU's load path drains while the matrix cores run.
@@ -354,17 +362,14 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
 #pragma unroll
         for (int i = 0; i < NQB; i++) ka[i] = *reinterpret_cast<const u32x4 *>(krow + i * 16);
 #pragma unroll
-        for (int i = 0; i < NQB; i += 2) {
+        for (int i = 0; i < NQB; i++)
             sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka[i]), qreg[i], sc, 0, 0, 0);
-            sc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka[i + 1]), qreg[i + 1], sc2, 0, 0, 0);
-        }
         __builtin_amdgcn_sched_group_barrier(0x0100, NQB, 0);   // all K reads
 #pragma unroll
         for (int i = 0; i < NQB; i++) {
             __builtin_amdgcn_sched_group_barrier(0x0020, 1, 0);   // one global load
             __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);   // one MFMA
         }
-        sc += sc2;
         // Online softmax in the exp2 domain: p = exp2(s * scale - m) with m the running
         // (scaled) reference max; the tile max is taken on raw scores (scale > 0).
         // A tile past this group's keys (its last step) runs the score stage on whatever

@@ -214,20 +214,16 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
                                                                pb[hh], o[db], 0, 0, 0);
             }
     };
-    // S^T = K Q^T for the tile in K buffer kb (two accumulation chains).
+    // S^T = K Q^T for the tile in K buffer kb (one accumulation chain: dependent MFMAs
+    // issue back to back).
     auto qk = [&](int kb) {
-        f32x16 s2;
 #pragma unroll
-        for (int e = 0; e < 16; e++) sc[e] = s2[e] = 0.0f;
+        for (int e = 0; e < 16; e++) sc[e] = 0.0f;
         const uint16_t *krow = &sm.k[kb][r32 * KROW + kg * 8];
 #pragma unroll
-        for (int i = 0; i < NQB; i += 2) {
-            const bf16x8 a0 = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + i * 16));
-            const bf16x8 a1 = as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + (i + 1) * 16));
-            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qreg[i], sc, 0, 0, 0);
-            s2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qreg[i + 1], s2, 0, 0, 0);
-        }
-        sc += s2;
+        for (int i = 0; i < NQB; i++)
+            sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(*reinterpret_cast<const u32x4 *>(krow + i * 16)),
+                                                         qreg[i], sc, 0, 0, 0);
     };
     // Online softmax of tile j's scores (exp2 domain, lazy rescale) -> pb. Only tiles
     // reaching past mask_from (the diagonal / last tiles) compare key positions.
