@@ -176,8 +176,8 @@ def main():
                     help="only copy a 512 MiB buffer 5 times (reference for rocprof byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, "
-              "'How the path would shard'); run it with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (decode would shard "
+              "by sequence or KV head with no exchange); run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
