@@ -81,7 +81,7 @@ typedef struct {
     const int32_t *positions;         /* [total_tokens] 0-based positions */
     const int32_t *query_start_loc;   /* [B+1] token offsets, or NULL: uniform max_query_len */
     const int32_t *block_tables;      /* [B][block_table_stride] 1-based page ids */
-    float scale;                      /* softmax scale, e.g. 1/sqrt(D) */
+    float scale;                      /* softmax scale, e.g. 1/sqrt(D); finite and > 0 */
     int32_t causal;                   /* 1: key i visible to query t iff i <= pos(t) */
     int32_t path;                     /* ti_path */
     void *workspace;                  /* split-KV partials; may be NULL for the prefill path */

@@ -93,6 +93,14 @@ def test_invalid_arguments(bad):
     assert ws(a, c)[0] == _lib.TI_ERR_INVALID_ARG
 
 
+def test_scale_must_be_finite_and_positive():
+    L = ti.load_library()
+    for bad in (0.0, -0.088, float("nan"), float("inf")):
+        a = _args(scale=bad)
+        assert L.ti_attention(ctypes.byref(a), ctypes.byref(_cache()), None) == _lib.TI_ERR_INVALID_ARG
+        assert ws(a, _cache())[0] == _lib.TI_ERR_INVALID_ARG
+
+
 def test_unsupported_shapes_and_workspace():
     L = ti.load_library()
     c = _cache(head_dim=96)

@@ -47,7 +47,9 @@ int check_attention(const ti_attention_args *a, const ti_kv_cache *c) {
     if (!a->query_start_loc && (long long)a->num_seqs * a->max_query_len != a->total_tokens)
         return TI_ERR_INVALID_ARG;
     if (a->causal != 0 && a->causal != 1) return TI_ERR_INVALID_ARG;
-    if (!(a->scale == a->scale)) return TI_ERR_INVALID_ARG;
+    // A finite positive softmax scale (1/sqrt(D) or a model's own): the MFMA kernels take
+    // each tile's running max on unscaled scores, which needs scale > 0.
+    if (!(a->scale > 0.0f) || a->scale == INFINITY) return TI_ERR_INVALID_ARG;
     // launch grids put sequences in a dimension of at most 65535
     if (a->num_seqs > 65535) return TI_ERR_UNSUPPORTED;
     return TI_OK;
