@@ -10,7 +10,7 @@ namespace {
 // Merge the splits of packed rows: grid (ceil(M / 4), Hk, B), four waves, one row per
 // wave; lane owns head-dim elements lane + 64 k. The running maxima and sums are
 // wave-uniform loads; the partial rows are read coalesced, with no LDS and no barrier.
-template <int D, typename T>
+template <int D, typename T, int SB>
 __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     constexpr int PER = D / 64;
     const int lane = threadIdx.x & 63;
@@ -23,9 +23,9 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     if (t >= nb) return;
     const size_t stride = (size_t)p.M * (D + 2);
     const float *base = p.part + ((size_t)b * p.Hk + h) * p.splits * stride + (size_t)r * (D + 2);
-    // Splits in batches of SB: every load of a batch (m, l and the row) is issued before
-    // any arithmetic, and batches merge online, so up to SB splits cost one round trip.
-    constexpr int SB = 8;
+    // Splits in batches of SB (2, 4 or 8: the launch takes the smallest that holds all
+    // splits, at most 8): every load of a batch (m, l and the row) is issued before any
+    // arithmetic, and batches merge online, so up to SB splits cost one round trip.
     float mx = NEG_BIG, lsum = 0.0f, acc[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) acc[k] = 0.0f;
@@ -60,6 +60,15 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     T *o = reinterpret_cast<T *>(p.out) + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
 #pragma unroll
     for (int k = 0; k < PER; k++) Elt<T>::st(o, lane + 64 * k, acc[k] * inv);
+}
+
+template <int D, typename T>
+void launch_combine_sb(const DecodeParams &p, int sb, dim3 grid, hipStream_t s) {
+    switch (sb) {
+        case 2: combine_kernel<D, T, 2><<<grid, 256, 0, s>>>(p); break;
+        case 4: combine_kernel<D, T, 4><<<grid, 256, 0, s>>>(p); break;
+        default: combine_kernel<D, T, 8><<<grid, 256, 0, s>>>(p); break;
+    }
 }
 
 template <int D, bool INT8, bool PG16, int NW>
@@ -183,12 +192,13 @@ int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows
     p.splits = splits;
     dim3 cgrid((rows + 3) / 4, c->kv_heads, a->num_seqs);
     const bool f32 = a->dtype == TI_F32;
+    const int sb = splits <= 2 ? 2 : (splits <= 4 ? 4 : 8);
     if (c->head_dim == 128) {
-        if (f32) combine_kernel<128, float><<<cgrid, 256, 0, s>>>(p);
-        else combine_kernel<128, uint16_t><<<cgrid, 256, 0, s>>>(p);
+        if (f32) launch_combine_sb<128, float>(p, sb, cgrid, s);
+        else launch_combine_sb<128, uint16_t>(p, sb, cgrid, s);
     } else {
-        if (f32) combine_kernel<64, float><<<cgrid, 256, 0, s>>>(p);
-        else combine_kernel<64, uint16_t><<<cgrid, 256, 0, s>>>(p);
+        if (f32) launch_combine_sb<64, float>(p, sb, cgrid, s);
+        else launch_combine_sb<64, uint16_t>(p, sb, cgrid, s);
     }
     return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
 }
