@@ -7,8 +7,9 @@ A step is one call of the headline workload: Qwen3-4B-shaped bf16 paged decode a
 batch of 32 sequences of 4096 cached positions, inputs resident in HBM. Two copies of the
 KV pools alternate between steps (2 x 537 MB, over 4x the 256 MB Infinity Cache) so every
 step streams its pages from HBM. Prints ONE JSON line: decode GB/s as `value`, with the
-prefill TFLOP/s, INT8-KV decode, speculative-verify and fused RoPE + KV-write figures of
-the other BASELINE configs alongside, the roofline of the decode kernel and the CPU
+decode figures at batch 1, 8 and 32 with context lengths drawn from [1024, 8192] (the
+config as stated), prefill TFLOP/s, INT8-KV decode, speculative-verify and fused RoPE +
+KV-write figures of the other BASELINE configs alongside, the roofline of the decode kernel and the CPU
 baseline (the oracle's Float32 op on the host cores, a bounded sample). The headline is
 timed call by call (HIP events around K steps); the other legs replay a HIP graph of 20
 captured calls, which removes host launch overhead from their microsecond-scale figures.
@@ -109,6 +110,36 @@ def decode_setup(B, L, n, Hq, Hk, D, P, copies, gen, int8=False, cold=True):
     return dict(pools=pools, bts=bts, q=q, out=out, pos=pos, ws=ws, n=n, B=B, L=L)
 
 
+def ragged_setup(B, Hq, Hk, D, P, seed):
+    """BASELINE configs[1] as stated: B sequences with context lengths drawn uniformly from
+    [1024, 8192] (seeded), one query token each at position L_b - 1, shuffled pages,
+    block tables as wide as the longest sequence (zero-padded), pool copies cycling past
+    the Infinity Cache."""
+    import numpy as np
+    import torch
+    import tileinfer_hip as ti
+    g = np.random.default_rng(seed)
+    lens = g.integers(1024, 8193, size=B)
+    per = -(-lens // P)
+    pages = int(per.sum())
+    copy_bytes = 2 * pages * Hk * P * 2 * D
+    copies = max(2, min(64, -(-2 * CACHE_BYTES // copy_bytes)))
+    perm = torch.from_numpy(g.permutation(pages).astype(np.int32) + 1)
+    bts = torch.zeros((B, int(per.max())), dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        bts[b, :per[b]] = perm[off:off + per[b]]
+        off += int(per[b])
+    pools = [(torch.randn((pages, Hk, P, D), device="cuda", dtype=torch.bfloat16),
+              torch.randn((pages, Hk, P, D), device="cuda", dtype=torch.bfloat16)) for _ in range(copies)]
+    q = torch.randn((B, Hq, D), device="cuda", dtype=torch.bfloat16)
+    pos = torch.from_numpy((lens - 1).astype(np.int32)).cuda()
+    ws = ti.attention_workspace(ti.HipBackend(), q, pools[0][0], num_seqs=B, max_query_len=1)
+    nbytes = int(lens.sum()) * 2 * Hk * D * 2 + B * 2 * Hq * D * 2
+    return dict(pools=pools, bts=bts.cuda(), q=q, out=torch.empty_like(q), pos=pos, ws=ws, n=1, B=B,
+                lens=lens, bytes=nbytes)
+
+
 def decode_call(s, i, scale, path=0):
     import tileinfer_hip as ti
     k, v = s["pools"][i % len(s["pools"])]
@@ -170,7 +201,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", default="",
-                    help="comma list: decode,fp32,verify,int8,prefill (= prefill512,chunked,prefill4096),kvwrite; "
+                    help="comma list: decode,ragged,fp32,verify,int8,prefill (= prefill512,chunked,prefill4096),kvwrite; "
                          "'none' runs the headline only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only copy a 512 MiB buffer 5 times (reference for rocprof byte counters)")
@@ -237,6 +268,17 @@ def main():
             bx = decode_bytes(Bx, L, 1, Hq, Hk, D, D * 2)
             extra[f"decode_b{Bx}"] = {"us": round(msx * 1e3, 2), "GB/s": round(bx / msx / 1e6, 1)}
             del sx
+    if want("decode") or want("ragged"):
+        for Bx in (1, 8, 32):
+            sx = ragged_setup(Bx, Hq, Hk, D, P, 20261201 + Bx)
+            msx = time_graph(lambda i: decode_call(sx, i, scale))
+            gx = sx["bytes"] / msx / 1e6
+            extra[f"decode_ragged_b{Bx}"] = {"us": round(msx * 1e3, 2), "GB/s": round(gx, 1),
+                                             "pct_hbm_peak": round(100 * gx / HBM_PEAK_GBS, 1),
+                                             "context_sum": int(sx["lens"].sum()), "context_max": int(sx["lens"].max())}
+            log(f"decode ragged B={Bx}: {msx * 1e3:.1f} us, {gx:.0f} GB/s")
+            del sx
+        torch.cuda.empty_cache()
     if want("fp32"):
         # configs[0]'s shape on the fp32 path: B = 1, 16 query / 8 KV heads, 1024 positions
         import tileinfer_hip as ti
