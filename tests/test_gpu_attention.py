@@ -93,6 +93,26 @@ def test_attention(gpu, case, bf16):
             check(ref, run_gpu(c, dtype, ti.TI_PATH_PREFILL), True)
 
 
+# The largest shapes the paths take: a 128k-token context (8192 pages of 16), one KV head
+# shared by 64 query heads (G = 64: 64 packed rows on the decode kernel, 192 on the
+# prefill kernel), head_dim 64 at G = 64, and a 16-query verify step on a 64k context.
+LIMIT_CASES = [(128, 8, 2, 16, 131071, 1, True), (128, 64, 1, 16, 5000, 1, True),
+               (128, 64, 1, 16, 3000, 3, True), (64, 64, 1, 16, 2000, 1, True),
+               (128, 8, 2, 16, 65543, 16, True)]
+
+
+@pytest.mark.parametrize("case", LIMIT_CASES, ids=str)
+def test_attention_limits(gpu, case):
+    D, H, KVH, P, start, n, causal = case
+    print(f"case {case}", flush=True)
+    c = make_case(case, True, seed=hash(case) % 10000 + 11)
+    ref = exact(c)
+    check(ref, run_gpu(c, torch.bfloat16), True)
+    if (H // KVH) * n <= 64:
+        check(ref, run_gpu(c, torch.bfloat16, ti.TI_PATH_DECODE), True)
+    check(ref, run_gpu(c, torch.bfloat16, ti.TI_PATH_PREFILL), True)
+
+
 @pytest.mark.parametrize("case", REF_CASES + EXTRA_CASES[:5], ids=str)
 def test_attention_int8(gpu, case):
     """INT8 cache (bf16 activations), keys scaled like the smoothing factors."""
