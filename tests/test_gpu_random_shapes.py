@@ -71,21 +71,25 @@ def test_random_shape(gpu, seed):
     runs = [(path, None) for path in paths]
     if kind == "bf16":
         # the prefill path through both prefill kernels (TI_PREFILL_PP=1 takes the 8-wave
-        # ping-pong kernel wherever its shape limits allow, =0 never)
-        runs += [(ti.TI_PATH_PREFILL, "1"), (ti.TI_PATH_PREFILL, "0")]
-    for path, pp in runs:
-        old = os.environ.get("TI_PREFILL_PP")
-        if pp is not None:
-            os.environ["TI_PREFILL_PP"] = pp
+        # ping-pong kernel wherever its shape limits allow, =0 never) and through both tile
+        # loaders of the four-wave kernel (TI_PREFILL_DL=0: register-staged loads, =1:
+        # direct global -> LDS loads wherever they apply)
+        runs += [(ti.TI_PATH_PREFILL, {"TI_PREFILL_PP": "1"}), (ti.TI_PATH_PREFILL, {"TI_PREFILL_PP": "0"}),
+                 (ti.TI_PATH_PREFILL, {"TI_PREFILL_PP": "0", "TI_PREFILL_DL": "0"}),
+                 (ti.TI_PATH_PREFILL, {"TI_PREFILL_PP": "0", "TI_PREFILL_DL": "1"})]
+    for path, env in runs:
+        env = env or {}
+        saved = {k: os.environ.get(k) for k in env}
+        os.environ.update(env)
         try:
             out = torch.full_like(qd, float("nan"))
             ws = ti.attention_workspace(BE, qd, k, path=path)
             ti.attention_(BE, out, ws, qd, k, v, btd, pos, scale, causal, path=path)
         finally:
-            if pp is not None:
-                if old is None:
-                    del os.environ["TI_PREFILL_PP"]
+            for key, val in saved.items():
+                if val is None:
+                    del os.environ[key]
                 else:
-                    os.environ["TI_PREFILL_PP"] = old
+                    os.environ[key] = val
         err = float(np.max(np.abs(ref - out.float().cpu().numpy())))
-        assert err <= tol, f"path {path} pp {pp}: max abs err {err}"
+        assert err <= tol, f"path {path} {env}: max abs err {err}"
