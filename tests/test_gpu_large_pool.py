@@ -104,3 +104,46 @@ def test_int8_pool_past_2_31_elements(gpu):
         _check(q, start, n, ref_fn, kq, vq, ids, [(ti.TI_PATH_AUTO, {}), (ti.TI_PATH_PREFILL, {})])
     del kq, vq
     torch.cuda.empty_cache()
+
+
+def test_fused_write_past_2_31_elements(gpu):
+    """attention_inputs_ (RoPE, theta 1e6, no norm) writing 512 tokens into pages past
+    element 2^31 of a bf16 and of an INT8 pool: the written pages are bit-identical to the
+    oracle's fused write into a compact pool (slots in the same page order)."""
+    g = rng(9300)
+    n, nq = 512, HQ
+    ids, _, _, _ = _setup(g)
+    ids = ids[: n // P]
+    positions = np.arange(n, dtype=np.int32)
+    slots = ((ids[positions // P] - 1) * P + positions % P + 1).astype(np.int32)
+    table = ti.RotaryTable.build(D, n, 1e6, torch.bfloat16)
+    cos_sin = table.cos_sin.float().cpu().numpy()
+    qkv = randn(g, n, nq + 2 * HK, D, bf16=True)
+    qkv_d = torch.from_numpy(qkv).bfloat16().cuda()
+    pos_d, slots_d = torch.from_numpy(positions).cuda(), torch.from_numpy(slots).cuda()
+    compact = np.arange(1, n + 1, dtype=np.int32)
+    sel = torch.from_numpy(ids - 1).long().cuda()
+
+    kd = torch.empty((PAGES, HK, P, D), dtype=torch.bfloat16, device="cuda")
+    vd = torch.empty_like(kd)
+    q = torch.empty((n, nq, D), dtype=torch.bfloat16, device="cuda")
+    ti.attention_inputs_(BE, q, kd, vd, qkv_d, None, None, table, pos_d, slots_d, 1e-6)
+    rkp = np.zeros((n // P, HK, P, D), np.float32)
+    rvp = np.zeros_like(rkp)
+    rq = orc.attention_inputs(qkv, None, None, cos_sin, positions, compact, nq, HK, 1e-6, True,
+                              k_pages=rkp, v_pages=rvp)
+    assert np.array_equal(q.float().cpu().numpy(), rq)
+    assert np.array_equal(kd[sel].float().cpu().numpy(), rkp)
+    assert np.array_equal(vd[sel].float().cpu().numpy(), rvp)
+    del kd, vd
+
+    kq, vq = ti.int8_kv_pools(D, P, HK, PAGES)
+    ti.attention_inputs_(BE, q, kq, vq, qkv_d, None, None, table, pos_d, slots_d, 1e-6)
+    lq = np.zeros((2, n // P, HK, P, D), np.int8)
+    ls = np.zeros((2, n // P, HK, P), np.float32)
+    orc.attention_inputs(qkv, None, None, cos_sin, positions, compact, nq, HK, 1e-6, True,
+                         layer_q=lq, layer_scale=ls, smooth=np.ones(D, np.float32))
+    assert np.array_equal(kq.layer_q[:, sel].cpu().numpy(), lq)
+    assert np.array_equal(kq.layer_scale[:, sel].cpu().numpy(), ls)
+    del kq, vq
+    torch.cuda.empty_cache()
