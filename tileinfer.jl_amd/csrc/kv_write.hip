@@ -293,19 +293,36 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
     using V = Vec4<T>;
     const int t = blockIdx.x, j = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
     if (j >= nq + nkv) return;   // a whole 16-lane group
-    const int pos = positions[t];
-    if (pos < 0 || pos >= table_len) return;
     const bool is_q = j < nq;
     const int h = j - nq;
-    long long row = 0;
-    if (!is_q) {
-        row = slot_row(slots[t], h, P, nkv, pages);
-        if (row < 0) return;
-    }
+    // Every load that does not depend on the position goes out first (token t < n and head
+    // j are in range, so these addresses are too): one memory round trip, then the rotary
+    // table rows of the position, instead of position -> slot -> qkv in sequence.
+    const int pos = positions[t];
+    const int32_t slot = slots[t];
     const size_t col = ((size_t)t * (nq + 2 * nkv) + j) * D;
     float a[4], b[4];
     V::ld(qkv + col + 4 * u, a);
     V::ld(qkv + col + HALF + 4 * u, b);
+    constexpr int VCH = D * (int)sizeof(T) / 16;   // 16-byte chunks of a value row
+    uint4 vrow[VCH / 16];
+    if (!is_q) {
+        const uint4 *vs = reinterpret_cast<const uint4 *>(qkv + ((size_t)t * (nq + 2 * nkv) + nq + nkv + h) * D);
+#pragma unroll
+        for (int c = 0; c < VCH / 16; c++) vrow[c] = vs[u + 16 * c];
+    }
+    float w1[4], w2[4];
+    if (NORM) {
+        const T *wn = is_q ? q_norm : k_norm;
+        V::ld(wn + 4 * u, w1);
+        V::ld(wn + HALF + 4 * u, w2);
+    }
+    if (pos < 0 || pos >= table_len) return;
+    long long row = 0;
+    if (!is_q) {
+        row = slot_row(slot, h, P, nkv, pages);
+        if (row < 0) return;
+    }
     if (NORM) {
         float pp[4];
 #pragma unroll
@@ -317,10 +334,6 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
         const float p02 = pp[0] + pp[2], p13 = pp[1] + pp[3];
         const float ss = p02 + p13;
         const float inv_rms = __frcp_rn(__fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
-        const T *wn = is_q ? q_norm : k_norm;
-        float w1[4], w2[4];
-        V::ld(wn + 4 * u, w1);
-        V::ld(wn + HALF + 4 * u, w2);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             a[e] = E::rnd(E::rnd(a[e] * inv_rms) * w1[e]);
@@ -342,11 +355,10 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
     V::st(dst + 4 * u, y1);
     V::st(dst + HALF + 4 * u, y2);
     if (is_q) return;
-    // the value row: a bit copy, D * sizeof(T) bytes in 16-byte chunks over the 16 lanes
-    const uint4 *vs = reinterpret_cast<const uint4 *>(qkv + ((size_t)t * (nq + 2 * nkv) + nq + nkv + h) * D);
+    // the value row (loaded above): a bit copy in 16-byte chunks over the 16 lanes
     uint4 *vd = reinterpret_cast<uint4 *>(vp + (size_t)row * D);
 #pragma unroll
-    for (int c = u; c < D * (int)sizeof(T) / 16; c += 16) vd[c] = vs[c];
+    for (int c = 0; c < VCH / 16; c++) vd[u + 16 * c] = vrow[c];
 }
 
 }  // namespace
