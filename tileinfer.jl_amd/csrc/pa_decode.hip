@@ -23,9 +23,9 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     if (t >= nb) return;
     const size_t stride = (size_t)p.M * (D + 2);
     const float *base = p.part + ((size_t)b * p.Hk + h) * p.splits * stride + (size_t)r * (D + 2);
-    // Splits in batches of SB (2, 4 or 8: the launch takes the smallest that holds all
-    // splits, at most 8): every load of a batch (m, l and the row) is issued before any
-    // arithmetic, and batches merge online, so up to SB splits cost one round trip.
+    // Splits in batches of SB (2, 4, 8 or 16: the launch takes the smallest that holds all
+    // splits): every load of a batch (m, l and the row) is issued before any arithmetic,
+    // and batches merge online, so up to SB splits cost one round trip.
     float mx = NEG_BIG, lsum = 0.0f, acc[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) acc[k] = 0.0f;
@@ -67,7 +67,8 @@ void launch_combine_sb(const DecodeParams &p, int sb, dim3 grid, hipStream_t s) 
     switch (sb) {
         case 2: combine_kernel<D, T, 2><<<grid, 256, 0, s>>>(p); break;
         case 4: combine_kernel<D, T, 4><<<grid, 256, 0, s>>>(p); break;
-        default: combine_kernel<D, T, 8><<<grid, 256, 0, s>>>(p); break;
+        case 8: combine_kernel<D, T, 8><<<grid, 256, 0, s>>>(p); break;
+        default: combine_kernel<D, T, 16><<<grid, 256, 0, s>>>(p); break;
     }
 }
 
@@ -195,7 +196,7 @@ int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows
     p.splits = splits;
     dim3 cgrid((rows + 3) / 4, c->kv_heads, a->num_seqs);
     const bool f32 = a->dtype == TI_F32;
-    const int sb = splits <= 2 ? 2 : (splits <= 4 ? 4 : 8);
+    const int sb = splits <= 2 ? 2 : (splits <= 4 ? 4 : (splits <= 8 ? 8 : 16));
     if (c->head_dim == 128) {
         if (f32) launch_combine_sb<128, float>(p, sb, cgrid, s);
         else launch_combine_sb<128, uint16_t>(p, sb, cgrid, s);
