@@ -266,7 +266,8 @@ def main():
             sx = decode_setup(Bx, L, 1, Hq, Hk, D, P, 2, gen)
             msx = time_graph(lambda i: decode_call(sx, i, scale))
             bx = decode_bytes(Bx, L, 1, Hq, Hk, D, D * 2)
-            extra[f"decode_b{Bx}"] = {"us": round(msx * 1e3, 2), "GB/s": round(bx / msx / 1e6, 1)}
+            extra[f"decode_b{Bx}"] = {"us": round(msx * 1e3, 2), "GB/s": round(bx / msx / 1e6, 1),
+                                      "pct_hbm_peak": round(100 * bx / msx / 1e6 / HBM_PEAK_GBS, 1)}
             del sx
     if want("decode") or want("ragged"):
         for Bx in (1, 8, 32):
