@@ -422,13 +422,23 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         // scheduling region; its PV stage is skipped.
         const bool valid = kt < kt_hi;
         const bool need_mask = !valid || kt * KT + KT - 1 > mask_from;
+        // INT8: the scales of this lane's 16 score keys, 8 q + 4 kg + (0..3) for q = 0..3,
+        // as four 16-B reads per array
+        f32x4 skq[4], svq[4];
+        if constexpr (INT8) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                skq[q] = *reinterpret_cast<const f32x4 *>(&sm.sk[buf][8 * q + 4 * kg]);
+                svq[q] = *reinterpret_cast<const f32x4 *>(&sm.sv[buf][8 * q + 4 * kg]);
+            }
+        }
         float x[16];
         float mt = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
             const int key = 8 * (e >> 2) + 4 * kg + (e & 3);
             float v = sc[e];
-            if (INT8) v *= sm.sk[buf][key];
+            if constexpr (INT8) v *= skq[e >> 2][e & 3];
             if (need_mask) {
                 const int kpos = kt * KT + key;
                 v = (valid && kpos <= qpos && kpos < kend) ? v : -INFINITY;
@@ -451,7 +461,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         for (int e = 0; e < 16; e++) {
             pe[e] = fast_exp2(__builtin_fmaf(x[e], p.scale_log2, -m));
             ps += pe[e];
-            if (INT8) pe[e] *= sm.sv[buf][8 * (e >> 2) + 4 * kg + (e & 3)];
+            if constexpr (INT8) pe[e] *= svq[e >> 2][e & 3];
         }
         l += ps;
         bf16x8 pb[2];
