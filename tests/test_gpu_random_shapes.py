@@ -32,7 +32,11 @@ def draw(g):
     return D, Hk, G, P, start, n, causal, kind
 
 
-@pytest.mark.parametrize("seed", list(range(int(os.environ.get("TI_RANDOM_SHAPES", "60")))))
+# TI_RANDOM_SHAPES cases from seed TI_RANDOM_SHAPES_FROM (default: 60 from seed 0)
+_FROM = int(os.environ.get("TI_RANDOM_SHAPES_FROM", "0"))
+
+
+@pytest.mark.parametrize("seed", list(range(_FROM, _FROM + int(os.environ.get("TI_RANDOM_SHAPES", "60")))))
 def test_random_shape(gpu, seed):
     g = rng(7000 + seed)
     D, Hk, G, P, start, n, causal, kind = draw(g)
