@@ -45,9 +45,24 @@ typedef enum { TI_F32 = 0, TI_BF16 = 1 } ti_dtype;      /* activations / dense p
 typedef enum { TI_KV_DENSE = 0, TI_KV_INT8 = 1 } ti_kv_kind;
 
 /* Path selection for ti_attention. AUTO follows the reference's rule
- * (src/ops/tile/attention.jl:265, :351-352): split-KV decode for steps of at most 16
- * query tokens, the prefill kernel otherwise. */
-typedef enum { TI_PATH_AUTO = 0, TI_PATH_DECODE = 1, TI_PATH_PREFILL = 2 } ti_path;
+ * (src/ops/tile/attention.jl:265, :351-352): split-KV decode for short steps, the prefill
+ * kernel otherwise. PREFILL takes the prefill family and lets the library pick its
+ * variant from host shapes; the last three pin one variant of it (for tests and tuning:
+ * every variant gives results within the same tolerances, and pinned variants that the
+ * shapes do not allow fall back to the library's pick):
+ *   PREFILL_STAGED    four-wave kernel, K/V tiles staged through registers into LDS
+ *   PREFILL_DIRECT    four-wave kernel, direct global -> LDS tile loads (bf16 dense cache,
+ *                     head_dim 128, pages of 2^k >= 16 tokens; otherwise staged)
+ *   PREFILL_PINGPONG  eight-wave ping-pong kernel (bf16 dense cache, head_dim 128, pages
+ *                     of 2^k >= 16 tokens, 256 % (q_heads / kv_heads) == 0) */
+typedef enum {
+    TI_PATH_AUTO = 0,
+    TI_PATH_DECODE = 1,
+    TI_PATH_PREFILL = 2,
+    TI_PATH_PREFILL_STAGED = 3,
+    TI_PATH_PREFILL_DIRECT = 4,
+    TI_PATH_PREFILL_PINGPONG = 5,
+} ti_path;
 
 /* One layer's KV cache: dense pools in the activations' type, or an INT8 layer
  * (Int8Pages pair: src/ops/quant.jl:86-92). Host struct of device pointers. */
@@ -68,7 +83,12 @@ typedef struct {
  * tokens [qsl[b], qsl[b+1]) of q (or [b*max_query_len, (b+1)*max_query_len) when
  * query_start_loc is NULL), its first query sits at positions[qsl[b]] and it attends to
  * keys 0 .. positions[qsl[b]] + n_b - 1 through block table row b. num_seqs = 1 is
- * exactly the reference's one-sequence op. */
+ * exactly the reference's one-sequence op.
+ * Contract on the device data (not checkable on the host): a row of block_tables must hold
+ * at least ceil(len / page_size) page ids for the sequence's len = positions[qsl[b]] + n_b
+ * keys, and n_b <= max_query_len. Out of contract, no access leaves the block-table row or
+ * the pool (page indices are clamped to [0, block_table_stride), page ids to the pool,
+ * n_b to max_query_len), but the output is unspecified. */
 typedef struct {
     int32_t dtype;                    /* ti_dtype of q, out (and dense pools) */
     int32_t q_heads;                  /* Hq; Hq % Hk == 0 */
@@ -145,7 +165,9 @@ int ti_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int h
  * rounding to T after every operation as the reference does.
  * Replaces rope!(::TileBackend, y, x, cos, sin, positions)
  * (src/ops/tile/elementwise.jl:10-36; reference src/ops/reference.jl:32-39).
- * cos_table, sin_table: [table_len][D]. Positions outside the table are skipped.
+ * cos_table, sin_table: [table_len][D]. Tokens whose position lies outside [0, table_len)
+ * are skipped: their rows of y are left untouched (the reference indexes past its table
+ * there; a kernel cannot raise, so the row keeps what it held).
  */
 int ti_rope(int dtype, void *y, const void *x, const void *cos_table, const void *sin_table,
             int table_len, const int32_t *positions, int n, int heads, int head_dim, void *stream);
@@ -158,7 +180,9 @@ int ti_rope(int dtype, void *y, const void *x, const void *cos_table, const void
  * table, positions, slots, eps) (src/ops/tile/fused.jl:94-130; generic chain
  * src/ops/interface.jl:169-179).
  * qkv: [n][q_heads + 2 Hk][D]; q_out: [n][q_heads][D]; q_norm, k_norm: [D] or both NULL;
- * cos_sin: [table_len][2][D].
+ * cos_sin: [table_len][2][D]. A token whose position lies outside [0, table_len) writes
+ * nothing (its q_out rows are left untouched and its K/V slot is not written); a token
+ * whose slot lies outside the pool writes no K/V row.
  */
 int ti_attention_inputs(int dtype, void *q_out, const ti_kv_cache *cache, const void *qkv,
                         const void *q_norm, const void *k_norm, const void *cos_sin,

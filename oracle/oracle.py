@@ -146,9 +146,6 @@ def _setup():
                                ctypes.c_int, I32, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
                                ctypes.c_int]
-    L.or_attention_f32_batch.argtypes = [F, F, F, F, I32, ctypes.c_int, I32, I32, ctypes.c_int,
-                                         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                         ctypes.c_float, ctypes.c_int, ctypes.c_int]
     L.or_bf16.restype = ctypes.c_float
     L.or_bf16.argtypes = [ctypes.c_float]
     lib_set = True
@@ -180,18 +177,39 @@ def attention(q, block_table, start, scale, causal=True, k_pages=None, v_pages=N
     return out
 
 
+_cpu_lib = None
+
+
+def cpu_lib():
+    """The CPU baseline (cpu_baseline.c), compiled for THIS host (-O3 -march=native
+    -ffast-math, OpenMP) into a private temporary directory on first use: the library
+    built for one machine's instruction set is never carried to another."""
+    global _cpu_lib
+    if _cpu_lib is None:
+        import tempfile
+        out = os.path.join(tempfile.mkdtemp(prefix="ti_cpu_baseline_"), "liboracle_cpu.so")
+        subprocess.run(["make", "-s", "-C", _HERE, f"CPU_LIB={out}", "cpu"], check=True)
+        L = ctypes.CDLL(out)
+        L.cb_attention_f32_batch.argtypes = [F, F, F, F, I32, ctypes.c_int, I32, I32, ctypes.c_int,
+                                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_float, ctypes.c_int, ctypes.c_int]
+        _cpu_lib = L
+    return _cpu_lib
+
+
 def attention_f32_batch(q, k_pages, v_pages, block_tables, starts, counts, scale, causal=True,
                         threads=None):
-    """CPU baseline: the eager op in Float32 over a batch, OpenMP over (sequence, head)."""
-    _setup()
+    """CPU baseline: the eager op in Float32 over a batch (cpu_baseline.c), OpenMP over
+    (sequence, KV head). Timed by bench.py; not a checker."""
     q = np.ascontiguousarray(q, np.float32)
     T, Hq, D = q.shape
     pages, Hk, P, _ = k_pages.shape
     out = np.empty_like(q)
     bts = np.ascontiguousarray(block_tables, np.int32)
     threads = threads or os.cpu_count() or 1
-    lib().or_attention_f32_batch(_f(out), _f(q), _f(k_pages), _f(v_pages), _i(bts), bts.shape[1],
-                                 _i(np.ascontiguousarray(starts, np.int32)),
-                                 _i(np.ascontiguousarray(counts, np.int32)), len(starts), Hq, Hk,
-                                 D, P, float(scale), int(causal), int(threads))
+    cpu_lib().cb_attention_f32_batch(_f(out), _f(q), _f(np.ascontiguousarray(k_pages, np.float32)),
+                                     _f(np.ascontiguousarray(v_pages, np.float32)), _i(bts), bts.shape[1],
+                                     _i(np.ascontiguousarray(starts, np.int32)),
+                                     _i(np.ascontiguousarray(counts, np.int32)), len(starts), Hq, Hk,
+                                     D, P, float(scale), int(causal), int(threads))
     return out

@@ -273,53 +273,3 @@ void or_attention(int mode, int bf16, float *out, const float *q, const float *k
     free(acc);
 }
 
-/*
- * CPU baseline: the same op in Float32 (the reference's eager op run on Float32
- * arrays, src/ops/reference.jl:95-121, gathered per KV head), over a batch of
- * sequences, OpenMP-parallel over (sequence, query head). Timed by bench.py only.
- * q/out: [sum n_b][Hq][D]; block tables [B][bt_stride]; starts[B], counts[B].
- */
-void or_attention_f32_batch(float *out, const float *q, const float *k_pages, const float *v_pages,
-                            const int32_t *bts, int bt_stride, const int32_t *starts,
-                            const int32_t *counts, int B, int Hq, int Hk, int D, int P,
-                            float scale, int causal, int threads) {
-    int *offs = (int *)malloc(sizeof(int) * (B + 1));
-    offs[0] = 0;
-    for (int b = 0; b < B; b++) offs[b + 1] = offs[b] + counts[b];
-    int G = Hq / Hk;
-#pragma omp parallel for collapse(2) schedule(dynamic) num_threads(threads)
-    for (int b = 0; b < B; b++)
-        for (int h = 0; h < Hq; h++) {
-            int start = starts[b], n = counts[b], len = start + n, g = h / G;
-            const int32_t *bt = bts + (size_t)b * bt_stride;
-            float *sc = (float *)malloc(sizeof(float) * len);
-            float *acc = (float *)malloc(sizeof(float) * D);
-            for (int t = 0; t < n; t++) {
-                const float *qv = q + ((size_t)(offs[b] + t) * Hq + h) * D;
-                int last = causal ? start + t : len - 1;
-                float mx = -INFINITY;
-                for (int i = 0; i <= last; i++) {
-                    const float *kr = k_pages + key_row(bt, i, g, P, Hk) * D;
-                    float s = 0.0f;
-                    for (int d = 0; d < D; d++) s += kr[d] * qv[d];
-                    sc[i] = s * scale;
-                    if (sc[i] > mx) mx = sc[i];
-                }
-                float sum = 0.0f;
-                for (int i = 0; i <= last; i++) {
-                    sc[i] = expf(sc[i] - mx);
-                    sum += sc[i];
-                }
-                for (int d = 0; d < D; d++) acc[d] = 0.0f;
-                for (int i = 0; i <= last; i++) {
-                    const float *vr = v_pages + key_row(bt, i, g, P, Hk) * D;
-                    float p = sc[i] / sum;
-                    for (int d = 0; d < D; d++) acc[d] += vr[d] * p;
-                }
-                memcpy(out + ((size_t)(offs[b] + t) * Hq + h) * D, acc, sizeof(float) * D);
-            }
-            free(sc);
-            free(acc);
-        }
-    free(offs);
-}

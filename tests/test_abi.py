@@ -124,16 +124,14 @@ def test_unsupported_shapes_and_workspace():
     assert L.ti_attention(ctypes.byref(a), ctypes.byref(c), None) == _lib.TI_ERR_UNSUPPORTED
     a = _args(q_heads=64, num_seqs=1, max_query_len=140000, total_tokens=140000)
     assert ws(a, c)[0] == _lib.TI_OK
-    old = os.environ.get("TI_PREFILL_PP")
-    os.environ["TI_PREFILL_PP"] = "0"
-    try:
+    # the four-wave kernel pinned: 70000 q-tiles exceed the grid
+    for path in (_lib.TI_PATH_PREFILL_STAGED, _lib.TI_PATH_PREFILL_DIRECT):
+        a = _args(q_heads=64, num_seqs=1, max_query_len=140000, total_tokens=140000, path=path)
         assert ws(a, c)[0] == _lib.TI_ERR_UNSUPPORTED
         assert L.ti_attention(ctypes.byref(a), ctypes.byref(c), None) == _lib.TI_ERR_UNSUPPORTED
-    finally:
-        if old is None:
-            del os.environ["TI_PREFILL_PP"]
-        else:
-            os.environ["TI_PREFILL_PP"] = old
+    a = _args(q_heads=64, num_seqs=1, max_query_len=140000, total_tokens=140000,
+              path=_lib.TI_PATH_PREFILL_PINGPONG)
+    assert ws(a, c)[0] == _lib.TI_OK
 
 
 def test_store_rope_inputs_validation():

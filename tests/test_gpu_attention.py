@@ -233,9 +233,10 @@ LOADER_CASES = [(128, 32, 8, 16, 0, 512, True, 1), (128, 32, 8, 16, 1024, 512, T
 
 
 @pytest.mark.parametrize("case", LOADER_CASES, ids=str)
-def test_prefill_tile_loaders_bit_identical(gpu, case, monkeypatch):
+def test_prefill_tile_loaders_bit_identical(gpu, case):
     """The four-wave prefill kernel's two tile loaders (register-staged loads + LDS stores,
-    TI_PREFILL_DL=0; direct global -> LDS loads into swizzled rows, TI_PREFILL_DL=1) feed
+    TI_PATH_PREFILL_STAGED; direct global -> LDS loads into swizzled rows,
+    TI_PATH_PREFILL_DIRECT) feed
     the same operands to the same arithmetic: outputs must be bit-identical, and within
     the tolerances of the oracle."""
     D, H, KVH, P, start, n, causal, B = case
@@ -253,16 +254,77 @@ def test_prefill_tile_loaders_bit_identical(gpu, case, monkeypatch):
     kd, vd = dev(kp, torch.bfloat16), dev(vp, torch.bfloat16)
     pos = torch.arange(start, L, dtype=torch.int32, device="cuda").repeat(B)
     outs = []
-    for dl in ("0", "1"):
-        monkeypatch.setenv("TI_PREFILL_DL", dl)
-        monkeypatch.setenv("TI_PREFILL_PP", "0")
-        ws = ti.attention_workspace(BE, qd, kd, num_seqs=B, max_query_len=n, path=ti.TI_PATH_PREFILL)
+    for path in (ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT):
+        ws = ti.attention_workspace(BE, qd, kd, num_seqs=B, max_query_len=n, path=path)
         out = torch.full_like(qd, float("nan"))
         ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(), pos, 1 / math.sqrt(D),
-                            causal, max_query_len=n, path=ti.TI_PATH_PREFILL)
+                            causal, max_query_len=n, path=path)
         outs.append(out)
     assert torch.equal(outs[0], outs[1])
     got = outs[1].float().cpu().numpy()
     for b in range(B):
         ref = orc.attention(q[b * n:(b + 1) * n], bts[b], start, 1 / math.sqrt(D), causal, kp, vp)
         assert float(np.max(np.abs(ref - got[b * n:(b + 1) * n]))) <= 2e-2
+
+
+# (head_dim, heads, kv_heads, page_size, start, n, table width in pages, dtype)
+NARROW_CASES = [(128, 32, 8, 16, 200, 1, 5, "bf16"), (128, 32, 8, 16, 0, 300, 7, "bf16"),
+                (128, 32, 8, 48, 100, 5, 1, "bf16"), (128, 32, 8, 16, 90, 16, 2, "bf16"),
+                (64, 8, 2, 16, 70, 3, 2, "fp32")]
+
+
+@pytest.mark.parametrize("case", NARROW_CASES, ids=str)
+def test_block_table_narrower_than_context(gpu, case):
+    """Out of contract: a block-table row holding fewer pages than the context needs. No
+    access may leave the row (the table tensor here is exactly that row, so a read past it
+    leaves the allocation); page indices past the row clamp to its last entry, so the
+    result equals attention over a table whose missing entries repeat that last page."""
+    D, H, KVH, P, start, n, width, kind = case
+    bf16 = kind == "bf16"
+    dtype = torch.bfloat16 if bf16 else torch.float32
+    g = rng(2100 + start + n + width)
+    L = start + n
+    pages = width + 4
+    bt = (g.permutation(pages)[:width] + 1).astype(np.int32)
+    need = -(-L // P)
+    bt_full = np.concatenate([bt, np.full(max(need - width, 0), bt[-1], np.int32)])
+    q = randn(g, n, H, D, bf16=bf16)
+    kp, vp = randn(g, pages, KVH, P, D, bf16=bf16), randn(g, pages, KVH, P, D, bf16=bf16)
+    ref = orc.attention(q, bt_full, start, 1 / math.sqrt(D), True, kp, vp)
+    qd, kd, vd = dev(q, dtype), dev(kp, dtype), dev(vp, dtype)
+    btd = torch.from_numpy(bt).cuda()
+    pos = torch.arange(start, L, dtype=torch.int32, device="cuda")
+    paths = [ti.TI_PATH_AUTO]
+    if bf16:
+        paths += ([ti.TI_PATH_DECODE] if n <= 16 else []) + [
+            ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT, ti.TI_PATH_PREFILL_PINGPONG]
+    for path in paths:
+        print(f"narrow table {case} path {path}", flush=True)
+        ws = ti.attention_workspace(BE, qd, kd, path=path)
+        out = torch.full_like(qd, float("nan"))
+        ti.attention_(BE, out, ws, qd, kd, vd, btd, pos, 1 / math.sqrt(D), True, path=path)
+        err = float(np.max(np.abs(ref - out.float().cpu().numpy())))
+        assert err <= TOL[bf16], f"path {path}: max abs err {err}"
+
+
+@pytest.mark.parametrize("n", [1, 40])
+def test_negative_position_reads_as_zero(gpu, n):
+    """Out of contract: a negative first position. The kernels read it as 0 (no access
+    before the block-table row or the pool), so the result is the start-0 attention."""
+    D, H, KVH, P = 128, 32, 8, 16
+    g = rng(2200 + n)
+    bt = block_table(g, n, P, 8)
+    q = randn(g, n, H, D, bf16=True)
+    kp, vp = randn(g, 8, KVH, P, D, bf16=True), randn(g, 8, KVH, P, D, bf16=True)
+    ref = orc.attention(q, bt, 0, 1 / math.sqrt(D), True, kp, vp)
+    qd, kd, vd = dev(q, torch.bfloat16), dev(kp, torch.bfloat16), dev(vp, torch.bfloat16)
+    # positions -50 .. : the kernels take the first; the step is n consecutive tokens
+    pos = torch.arange(-50, -50 + n, dtype=torch.int32, device="cuda")
+    for path in (ti.TI_PATH_AUTO, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT):
+        print(f"negative position n {n} path {path}", flush=True)
+        ws = ti.attention_workspace(BE, qd, kd, path=path)
+        out = torch.full_like(qd, float("nan"))
+        ti.attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bt).cuda(), pos, 1 / math.sqrt(D), True,
+                      path=path)
+        err = float(np.max(np.abs(ref - out.float().cpu().numpy())))
+        assert err <= 2e-2, f"path {path}: max abs err {err}"

@@ -42,21 +42,17 @@ def _check(q, start, n, ref_fn, kd, vd, bt, paths):
     qd = torch.from_numpy(q).bfloat16().cuda()
     pos = torch.arange(start, start + n, dtype=torch.int32, device="cuda")
     btd = torch.from_numpy(bt).cuda()
-    for path, env in paths:
-        with pytest.MonkeyPatch.context() as mp:
-            for key, val in env.items():
-                mp.setenv(key, val)
-            ws = ti.attention_workspace(BE, qd, kd, path=path)
-            out = torch.full_like(qd, float("nan"))
-            ti.attention_(BE, out, ws, qd, kd, vd, btd, pos, scale, True, path=path)
-            err = float(np.max(np.abs(ref - out.float().cpu().numpy())))
-        assert err <= 2e-2, f"start {start} n {n} path {path} {env}: max abs err {err}"
+    for path in paths:
+        ws = ti.attention_workspace(BE, qd, kd, path=path)
+        out = torch.full_like(qd, float("nan"))
+        ti.attention_(BE, out, ws, qd, kd, vd, btd, pos, scale, True, path=path)
+        err = float(np.max(np.abs(ref - out.float().cpu().numpy())))
+        assert err <= 2e-2, f"start {start} n {n} path {path}: max abs err {err}"
 
 
 # (start, n): decode, a 512-token prefill on a cached prefix, the verify shape
 STEPS = [(L - 1, 1), (L - 512, 512), (L - 16, 16)]
-PATHS = [(ti.TI_PATH_AUTO, {}), (ti.TI_PATH_PREFILL, {"TI_PREFILL_DL": "0"}),
-         (ti.TI_PATH_PREFILL, {"TI_PREFILL_DL": "1"})]
+PATHS = [ti.TI_PATH_AUTO, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT]
 
 
 def test_bf16_pool_past_2_31_elements(gpu):
@@ -76,7 +72,7 @@ def test_bf16_pool_past_2_31_elements(gpu):
     for start, n in STEPS:
         q = randn(g, n, HQ, D, bf16=True)
         ref_fn = lambda qq, s, sc: orc.attention(qq, bt_c, s, sc, True, kp_c, vp_c)
-        paths = PATHS if n > 1 else PATHS[:1] + [(ti.TI_PATH_DECODE, {})]
+        paths = PATHS if n > 1 else PATHS[:1] + [ti.TI_PATH_DECODE]
         _check(q, start, n, ref_fn, kd, vd, ids, paths)
     del kd, vd
     torch.cuda.empty_cache()
@@ -101,7 +97,7 @@ def test_int8_pool_past_2_31_elements(gpu):
     for start, n in STEPS:
         q = randn(g, n, HQ, D, bf16=True)
         ref_fn = lambda qq, s, sc: orc.attention(qq, bt_c, s, sc, True, layer_q=lq, layer_scale=ls, smooth=cs)
-        _check(q, start, n, ref_fn, kq, vq, ids, [(ti.TI_PATH_AUTO, {}), (ti.TI_PATH_PREFILL, {})])
+        _check(q, start, n, ref_fn, kq, vq, ids, [ti.TI_PATH_AUTO, ti.TI_PATH_PREFILL])
     del kq, vq
     torch.cuda.empty_cache()
 

@@ -1,6 +1,6 @@
 """The 8-wave ping-pong prefill kernel (pa_prefill_pp.hip) against the oracle.
 
-AUTO takes it only for large grids (a 4096-token prefill); TI_PREFILL_PP=1 forces it for
+AUTO takes it only for large grids (a 4096-token prefill); TI_PATH_PREFILL_PINGPONG pins it for
 every shape it accepts (bf16 dense cache, head_dim 128, power-of-two pages of >= 16
 tokens, heads per KV head dividing 256), so these cases cover its masks, ragged last
 tiles, key splits, the prologue with one or two key tiles and batched calls. Tolerance:
@@ -9,7 +9,6 @@ reference's bound, test/ops/tile.jl:237-259) up to 512 query tokens, the longest
 cases hold: longer causal prefills round more probabilities to bf16 and both prefill
 kernels reach 5.0-5.7 ulps at 1024-2048 tokens (same elements, same errors)."""
 import math
-import os
 
 import numpy as np
 import pytest
@@ -23,15 +22,8 @@ pytestmark = pytest.mark.gpu
 BE = ti.HipBackend()
 
 
-@pytest.fixture
-def force_pp():
-    old = os.environ.get("TI_PREFILL_PP")
-    os.environ["TI_PREFILL_PP"] = "1"
-    yield
-    if old is None:
-        del os.environ["TI_PREFILL_PP"]
-    else:
-        os.environ["TI_PREFILL_PP"] = old
+# Every call pins the ping-pong kernel (TI_PATH_PREFILL_PINGPONG).
+PP = ti.TI_PATH_PREFILL_PINGPONG
 
 
 # (heads, kv_heads, page_size, start, n, causal, block-table width in pages or 0)
@@ -52,7 +44,7 @@ CASES = [(32, 8, 16, 0, 1, True, 0),          # one key tile, one query
 
 
 @pytest.mark.parametrize("case", CASES, ids=str)
-def test_prefill_pp(gpu, force_pp, case):
+def test_prefill_pp(gpu, case):
     H, KVH, P, start, n, causal, width = case
     D = 128
     g = rng(4400 + start + n + H)
@@ -72,9 +64,9 @@ def test_prefill_pp(gpu, force_pp, case):
     btd = torch.from_numpy(bt).cuda()
     print(f"case {case}", flush=True)
     for with_ws in (True, False):
-        ws = ti.attention_workspace(BE, qd, kd, path=ti.TI_PATH_PREFILL) if with_ws else None
+        ws = ti.attention_workspace(BE, qd, kd, path=PP) if with_ws else None
         out = torch.full_like(qd, float("nan"))
-        ti.attention_(BE, out, ws, qd, kd, vd, btd, pos, 1 / math.sqrt(D), causal, path=ti.TI_PATH_PREFILL)
+        ti.attention_(BE, out, ws, qd, kd, vd, btd, pos, 1 / math.sqrt(D), causal, path=PP)
         got = out.float().cpu().numpy()
         err = float(np.max(np.abs(ref - got)))
         assert err <= 2e-2, f"workspace {with_ws}: max abs err {err}"
@@ -82,7 +74,7 @@ def test_prefill_pp(gpu, force_pp, case):
             assert ulps(ref, got) <= 5
 
 
-def test_prefill_pp_nan_pages(gpu, force_pp):
+def test_prefill_pp_nan_pages(gpu):
     """Keys past the step's last key in its last tile read allocated pool rows that may
     hold any bits: NaN there must not reach the output (their values are zeroed)."""
     H, KVH, P, D, start, n = 32, 8, 16, 128, 0, 40
@@ -101,13 +93,13 @@ def test_prefill_pp_nan_pages(gpu, force_pp):
     out = torch.empty_like(qd)
     ti.attention_(BE, out, None, qd, kd, vd, torch.from_numpy(bt).cuda(),
                   torch.arange(start, start + n, dtype=torch.int32, device="cuda"), 1 / math.sqrt(D), True,
-                  path=ti.TI_PATH_PREFILL)
+                  path=PP)
     got = out.float().cpu().numpy()
     assert np.isfinite(got).all()
     assert float(np.max(np.abs(ref - got))) <= 2e-2
 
 
-def test_prefill_pp_batched(gpu, force_pp):
+def test_prefill_pp_batched(gpu):
     """Ragged batch (one empty sequence) in one call."""
     g = rng(4600)
     D, H, KVH, P = 128, 32, 8, 16
@@ -129,11 +121,11 @@ def test_prefill_pp_batched(gpu, force_pp):
     qd = torch.from_numpy(q).bfloat16().cuda()
     out = torch.zeros_like(qd)
     kd, vd = torch.from_numpy(kp).bfloat16().cuda(), torch.from_numpy(vp).bfloat16().cuda()
-    ws = ti.attention_workspace(BE, qd, kd, num_seqs=len(starts), max_query_len=nmax, path=ti.TI_PATH_PREFILL)
+    ws = ti.attention_workspace(BE, qd, kd, num_seqs=len(starts), max_query_len=nmax, path=PP)
     ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(),
                         torch.from_numpy(positions).cuda(), 1 / math.sqrt(D), True,
                         query_start_loc=torch.from_numpy(qsl).cuda(), max_query_len=nmax,
-                        path=ti.TI_PATH_PREFILL)
+                        path=PP)
     got = out.float().cpu().numpy()
     for b, (s, n) in enumerate(zip(starts, counts)):
         if n == 0:

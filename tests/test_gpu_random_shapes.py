@@ -72,28 +72,15 @@ def test_random_shape(gpu, seed):
             paths.append(ti.TI_PATH_DECODE)
         paths.append(ti.TI_PATH_PREFILL)
     tol = 1e-4 if kind == "fp32" else 2e-2
-    runs = [(path, None) for path in paths]
     if kind == "bf16":
-        # the prefill path through both prefill kernels (TI_PREFILL_PP=1 takes the 8-wave
-        # ping-pong kernel wherever its shape limits allow, =0 never) and through both tile
-        # loaders of the four-wave kernel (TI_PREFILL_DL=0: register-staged loads, =1:
-        # direct global -> LDS loads wherever they apply)
-        runs += [(ti.TI_PATH_PREFILL, {"TI_PREFILL_PP": "1"}), (ti.TI_PATH_PREFILL, {"TI_PREFILL_PP": "0"}),
-                 (ti.TI_PATH_PREFILL, {"TI_PREFILL_PP": "0", "TI_PREFILL_DL": "0"}),
-                 (ti.TI_PATH_PREFILL, {"TI_PREFILL_PP": "0", "TI_PREFILL_DL": "1"})]
-    for path, env in runs:
-        env = env or {}
-        saved = {k: os.environ.get(k) for k in env}
-        os.environ.update(env)
-        try:
-            out = torch.full_like(qd, float("nan"))
-            ws = ti.attention_workspace(BE, qd, k, path=path)
-            ti.attention_(BE, out, ws, qd, k, v, btd, pos, scale, causal, path=path)
-        finally:
-            for key, val in saved.items():
-                if val is None:
-                    del os.environ[key]
-                else:
-                    os.environ[key] = val
+        # the prefill path through both prefill kernels (PINGPONG takes the 8-wave kernel
+        # wherever its shape limits allow) and through both tile loaders of the four-wave
+        # kernel (STAGED: register-staged loads; DIRECT: direct global -> LDS loads
+        # wherever they apply)
+        paths += [ti.TI_PATH_PREFILL_PINGPONG, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT]
+    for path in paths:
+        out = torch.full_like(qd, float("nan"))
+        ws = ti.attention_workspace(BE, qd, k, path=path)
+        ti.attention_(BE, out, ws, qd, k, v, btd, pos, scale, causal, path=path)
         err = float(np.max(np.abs(ref - out.float().cpu().numpy())))
-        assert err <= tol, f"path {path} {env}: max abs err {err}"
+        assert err <= tol, f"path {path}: max abs err {err}"

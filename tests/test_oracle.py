@@ -262,11 +262,69 @@ def test_attention_inputs_composes_rope_and_store():
     orc.store_kv(kp2, vp2, orc.rope(qkv[:, nq:nq + nkv], c, s, positions, True),
                  qkv[:, nq + nkv:].copy(), slots)
     assert np.array_equal(kp, kp2) and np.array_equal(vp, vp2)
-    # with q/k norm: rmsnorm in float64 then rope, within one bf16 rounding
+
+
+def _torch_norm_rope(x, w, c, s, pos, eps):
+    """Qwen3 q/k RMSNorm then rope with torch ops: inv_rms in Float32, x inv_rms rounded to
+    bf16, times w rounded to bf16 (src/ops/reference.jl:17-21, src/ops/tile/fused.jl:15-34),
+    then rope with every bf16 op rounding (src/ops/reference.jl:32-39)."""
+    x32 = torch.from_numpy(x).float()
+    inv = 1.0 / torch.sqrt((x32 * x32).sum(-1, keepdim=True) / x.shape[-1] + eps)
+    h = x.shape[-1] // 2
+    tx = (x32 * inv).bfloat16() * torch.from_numpy(w).bfloat16()
+    tc = torch.from_numpy(c[pos]).bfloat16()[:, None, :]
+    ts = torch.from_numpy(s[pos]).bfloat16()[:, None, :]
+    rot = torch.cat([-tx[..., h:], tx[..., :h]], -1)
+    return (tx * tc + rot * ts).float().numpy()
+
+
+def test_attention_inputs_norm_rounding_points():
+    # With q/k norm: the oracle's rounding points equal torch bf16 ops exactly. The sums of
+    # squares are made exact in any order (bf16 inputs that are small multiples of 1/8,
+    # so every square and partial sum is a float32 integer multiple of 1/64), so inv_rms
+    # is the same Float32 number on both sides and no tolerance is needed.
+    g = rng(24)
+    D, nq, nkv, P, pages = 128, 4, 2, 16, 6
+    positions = np.array([3, 17, 18, 40, 0, 63], np.int32)
+    slots = np.array([13, 14, 15, 16, 70, 2], np.int32)
+    n = len(positions)
+    theta = g.random((64, D // 2), dtype=np.float32) * 100
+    c = orc.bf16_round(np.cos(np.concatenate([theta, theta], 1)))
+    s = orc.bf16_round(np.sin(np.concatenate([theta, theta], 1)))
+    cs = np.stack([c, s], 1)
+    qkv = (g.integers(-64, 65, (n, nq + 2 * nkv, D)) / 8.0).astype(np.float32)
     qn, kn = randn(g, D, bf16=True), randn(g, D, bf16=True)
-    q = orc.attention_inputs(qkv, qn, kn, cs, positions, slots, nq, nkv, 1e-6, True,
-                             k_pages=kp, v_pages=vp)
-    x = qkv[:, :nq].astype(np.float64)
-    normed = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + 1e-6) * qn
-    want = orc.rope(normed.astype(np.float32), c.astype(np.float32), s.astype(np.float32), positions, False)
-    assert np.max(np.abs(q - want)) <= 0.05 * np.max(np.abs(want))
+    kp = np.zeros((pages, nkv, P, D), np.float32)
+    vp = np.zeros_like(kp)
+    for eps in (1e-6, 0.25):
+        q = orc.attention_inputs(qkv, qn, kn, cs, positions, slots, nq, nkv, eps, True,
+                                 k_pages=kp, v_pages=vp)
+        assert np.array_equal(q, _torch_norm_rope(qkv[:, :nq], qn, c, s, positions, eps))
+        k_want = _torch_norm_rope(qkv[:, nq:nq + nkv], kn, c, s, positions, eps)
+        for t, sl in enumerate(slots):
+            page, off = (sl - 1) // P, (sl - 1) % P
+            if page < pages:
+                assert np.array_equal(kp[page, :, off], k_want[t])
+                assert np.array_equal(vp[page, :, off], qkv[t, nq + nkv:])
+
+
+def test_attention_inputs_norm_random_within_one_ulp():
+    # Random bf16 inputs: the sum of squares' order differs (the oracle sums in double),
+    # so inv_rms may differ by a Float32 ulp: within one bf16 ulp of torch everywhere,
+    # equal almost everywhere.
+    g = rng(25)
+    D, nq, nkv, P, pages = 128, 8, 2, 16, 4
+    positions = g.integers(0, 64, 40).astype(np.int32)
+    n = len(positions)
+    theta = g.random((64, D // 2), dtype=np.float32) * 100
+    c = orc.bf16_round(np.cos(np.concatenate([theta, theta], 1)))
+    s = orc.bf16_round(np.sin(np.concatenate([theta, theta], 1)))
+    qkv = randn(g, n, nq + 2 * nkv, D, bf16=True, scale=3.0)
+    qn = randn(g, D, bf16=True)
+    kp = np.zeros((pages, nkv, P, D), np.float32)
+    q = orc.attention_inputs(qkv, qn, qn, np.stack([c, s], 1), positions, np.arange(1, n + 1, dtype=np.int32), nq, nkv,
+                             1e-6, True, k_pages=kp, v_pages=kp.copy())
+    want = _torch_norm_rope(qkv[:, :nq], qn, c, s, positions, 1e-6)
+    from helpers import bf16_eps
+    assert np.all(np.abs(q - want) <= bf16_eps(want) + 1e-30)
+    assert np.mean(q == want) >= 0.99

@@ -31,7 +31,10 @@ int resolve_path(const ti_attention_args *a, const ti_kv_cache *c) {
     switch (a->path) {
         case TI_PATH_AUTO: return decode_auto ? 1 : (G <= 64 ? 2 : -TI_ERR_UNSUPPORTED);
         case TI_PATH_DECODE: return decode_ok ? 1 : -TI_ERR_UNSUPPORTED;
-        case TI_PATH_PREFILL: return G <= 64 ? 2 : -TI_ERR_UNSUPPORTED;
+        case TI_PATH_PREFILL:
+        case TI_PATH_PREFILL_STAGED:
+        case TI_PATH_PREFILL_DIRECT:
+        case TI_PATH_PREFILL_PINGPONG: return G <= 64 ? 2 : -TI_ERR_UNSUPPORTED;
         default: return -TI_ERR_INVALID_ARG;
     }
 }

@@ -74,9 +74,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Block-table lookup with the 1-based page id clamped into the pool, so a malformed
-// table can never send a load outside the pool.
-__device__ __forceinline__ int page_of(const int32_t *bt, int idx, int num_pages) {
+// Block-table lookup: the index is clamped into the sequence's row [0, bt_stride) and the
+// 1-based page id into the pool, so neither a malformed table nor a position past the
+// table's width (or a negative one) can send a load outside the table or the pool.
+__device__ __forceinline__ int page_of(const int32_t *bt, int idx, int bt_stride, int num_pages) {
+    idx = idx < 0 ? 0 : (idx >= bt_stride ? bt_stride - 1 : idx);
     int p = bt[idx] - 1;
     p = p < 0 ? 0 : p;
     return p >= num_pages ? num_pages - 1 : p;
@@ -85,8 +87,9 @@ __device__ __forceinline__ int page_of(const int32_t *bt, int idx, int num_pages
 // The same lookup for a wave-uniform index, as a scalar load through the constant address
 // space: it is counted by lgkmcnt, so waiting for it never waits for the vector loads of
 // prefetched tiles (vmcnt is in order).
-__device__ __forceinline__ int page_of_s(const int32_t *bt, int idx, int num_pages) {
+__device__ __forceinline__ int page_of_s(const int32_t *bt, int idx, int bt_stride, int num_pages) {
     idx = __builtin_amdgcn_readfirstlane(idx);
+    idx = idx < 0 ? 0 : (idx >= bt_stride ? bt_stride - 1 : idx);
     const __attribute__((address_space(4))) int32_t *cbt =
         (const __attribute__((address_space(4))) int32_t *)bt;
     int p = cbt[idx] - 1;
@@ -124,6 +127,7 @@ int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows
 
 struct ti_prefill_plan {
     int pp;          // 1: the 8-wave ping-pong kernel (pa_prefill_pp.hip)
+    int dl;          // 1: direct global -> LDS tile loads in the four-wave kernel
     int wpg;         // waves per key group (32 packed rows each)
     int ng;          // key groups per work-group
     int splits;      // key splits across work-groups (partials merged by the combine kernel)

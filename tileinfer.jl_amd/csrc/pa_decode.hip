@@ -18,7 +18,7 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     const int h = blockIdx.y, b = blockIdx.z;
     if (r >= p.M) return;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
+    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
     const int t = r / p.G, g = r - t * p.G;
     if (t >= nb) return;
     const size_t stride = (size_t)p.M * (D + 2);

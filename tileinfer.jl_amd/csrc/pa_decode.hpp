@@ -95,7 +95,7 @@ struct TileRegs {
 // with the position clamped into the sequence (rows past len are never used unmasked).
 struct RowMap {
     const int32_t *bt;
-    int P, pshift, Hk, h, num_pages, len;
+    int P, pshift, Hk, h, num_pages, len, bt_stride;
     __device__ __forceinline__ int page_index(int pos) const {
         return pshift >= 0 ? (pos >> pshift) : pos / P;
     }
@@ -104,13 +104,13 @@ struct RowMap {
     }
     __device__ __forceinline__ long long row(int pos) const {
         pos = min(pos, len - 1);
-        const int pg = page_of(bt, page_index(pos), num_pages);
+        const int pg = page_of(bt, page_index(pos), bt_stride, num_pages);
         return ((long long)pg * Hk + h) * P + page_offset(pos);
     }
     // pos wave-uniform, P a power of two: scalar block-table load, shifts only
     __device__ __forceinline__ long long row_s(int pos) const {
         pos = min(pos, len - 1);
-        const int pg = page_of_s(bt, pos >> pshift, num_pages);
+        const int pg = page_of_s(bt, pos >> pshift, bt_stride, num_pages);
         return ((long long)pg * Hk + h) * P + (pos & (P - 1));
     }
 };
@@ -211,15 +211,15 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     const int row0 = rslice * MP;
     const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
+    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
     if (nb <= 0) return;
-    const int start = p.positions[tok0], len = start + nb;
+    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
     const int ntiles = (len + 15) >> 4;
     const int per = (ntiles + p.splits - 1) / p.splits;
     const int j0 = s * per, j1 = min(j0 + per, ntiles);
     const size_t half_q = (size_t)p.num_pages * p.Hk * p.P * D;
     const size_t half_s = (size_t)p.num_pages * p.Hk * p.P;
-    const RowMap rm{p.bt + (size_t)b * p.bt_stride, p.P, p.pshift, p.Hk, h, p.num_pages, len};
+    const RowMap rm{p.bt + (size_t)b * p.bt_stride, p.P, p.pshift, p.Hk, h, p.num_pages, len, p.bt_stride};
     // Keys up to mask_from are visible to every row; later tiles need the mask.
     const int mask_from = p.causal ? start : len - 1;
 

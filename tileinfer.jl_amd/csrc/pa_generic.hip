@@ -35,9 +35,9 @@ __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) 
     const int t = blockIdx.x / p.splits, split = blockIdx.x % p.splits;
     const int hq = blockIdx.y, b = blockIdx.z, lane = threadIdx.x;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
+    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
     if (t >= nb) return;
-    const int start = p.positions[tok0], len = start + nb;
+    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
     const int last = p.causal ? start + t : len - 1;
     // this split's keys: [k0, k1) of the sequence's len, cut at the query's last key
     const int per = (len + p.splits - 1) / p.splits;
@@ -65,7 +65,7 @@ __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) 
         float s = -INFINITY;
         long long row = 0;
         if (valid) {
-            const int pg = page_of(bt, key / p.P, p.num_pages);
+            const int pg = page_of(bt, key / p.P, p.bt_stride, p.num_pages);
             row = ((long long)pg * p.Hk + g) * p.P + key % p.P;
             float dot = 0.0f;
             if (INT8) {

@@ -89,7 +89,7 @@ __device__ __forceinline__ long long key_row(const PrefillParams &p, const int32
     pos = min(pos, kend - 1);
     const int idx = p.pshift >= 0 ? pos >> p.pshift : pos / p.P;
     const int off = p.pshift >= 0 ? pos & (p.P - 1) : pos % p.P;
-    const int pg = page_of(bt, idx, p.num_pages);
+    const int pg = page_of(bt, idx, p.bt_stride, p.num_pages);
     return ((long long)pg * p.Hk + h) * p.P + off;
 }
 
@@ -109,7 +109,7 @@ struct TileRows {
             for (int x = 0; x < 2; x++) {
                 const int pos = min(kt * KT + 16 * x, kend - 1);
                 const int idx = pos >> pp.pshift, off = pos & (pp.P - 1);   // PG16: P is 2^pshift
-                const int pg = page_of_s(btp, idx, pp.num_pages);
+                const int pg = page_of_s(btp, idx, pp.bt_stride, pp.num_pages);
                 half_row[x] = ((long long)pg * pp.Hk + hh) * pp.P + (off & ~15);
             }
         }
@@ -146,8 +146,7 @@ __device__ __forceinline__ TilePages tile_pages(const PrefillParams &p, const in
 #pragma unroll
     for (int x = 0; x < 2; x++) {
         const int pos = kt * KT + 16 * x;
-        const int idx = min(pos >> p.pshift, p.bt_stride - 1);   // only PG16 tiles: P = 2^pshift
-        tp.pg[x] = page_of_s(bt, idx, p.num_pages);
+        tp.pg[x] = page_of_s(bt, pos >> p.pshift, p.bt_stride, p.num_pages);   // PG16: P = 2^pshift
     }
     return tp;
 }
@@ -302,10 +301,10 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     const int split = (int)blockIdx.y % p.splits;
     const int b = blockIdx.z;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
+    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
     const int t_first = qt * p.TQ;
     if (t_first >= nb) return;
-    const int start = p.positions[tok0], len = start + nb;
+    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
     const int t_last = min(t_first + p.TQ, nb) - 1;
     const int kend = p.causal ? start + t_last + 1 : len;
     const int nkt = (kend + KT - 1) / KT;
@@ -743,12 +742,13 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     // when its work-groups fill the 256 CUs at least twice without key splits: measured
     // 906 vs 745 TFLOP/s at a 4096-token causal prefill (512 work-groups), but slower
     // at 2048 tokens (256) and below, where the four-wave kernel's smaller q-tiles and
-    // in-work-group key groups keep more CUs busy. TI_PREFILL_PP=1 takes it whenever the
-    // shapes allow, TI_PREFILL_PP=0 never (tuning and tests; read per call).
-    const char *pp_env = getenv("TI_PREFILL_PP");
-    const int pp_force = pp_env ? atoi(pp_env) : -1;
+    // in-work-group key groups keep more CUs busy. TI_PATH_PREFILL_PINGPONG pins it
+    // wherever the shapes allow; the other pinned variants never take it.
     const long long pp_wgs = (long long)((a->max_query_len + 256 / G - 1) / (256 / G)) * pairs;
-    pl.pp = ti_prefill_pp_eligible(a, c) && (pp_force == 1 || (pp_force != 0 && pp_wgs >= 512));
+    const bool pp_ok = ti_prefill_pp_eligible(a, c);
+    pl.pp = pp_ok && (a->path == TI_PATH_PREFILL_PINGPONG ||
+                      ((a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO) && pp_wgs >= 512));
+    pl.dl = 0;
     if (pl.pp) {
         // Key splits (forced runs on small grids) while work-groups are fewer than the
         // CUs and every split keeps at least 8 key tiles of the longest context the
@@ -782,6 +782,14 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
            (!bound_keys || key_tiles / (2 * pl.splits) >= 4LL * pl.ng))
         pl.splits *= 2;
     if (forced_splits >= 1 && forced_splits <= 64) pl.splits = forced_splits;
+    // Direct global -> LDS tile loads (bf16 dense cache, head_dim 128, pages of 2^k >= 16
+    // tokens) for two-wave key groups, the small grids: measured 13.8 -> 12.4 us at a
+    // 512-token prefill and 25.6 -> 23.3 us chunked, bit-identical; for four-wave groups
+    // (1024-3072 tokens) no change, so those keep the register-staged loads.
+    const bool dl_ok = c->kind == TI_KV_DENSE && a->dtype == TI_BF16 && c->head_dim == 128 &&
+                       c->page_size >= 16 && (c->page_size & (c->page_size - 1)) == 0;
+    pl.dl = dl_ok && (a->path == TI_PATH_PREFILL_DIRECT ||
+                      (a->path != TI_PATH_PREFILL_STAGED && pl.wpg == 2));
     pl.rows = G * a->max_query_len;
     pl.bytes = pl.splits == 1 ? 0 : (size_t)pairs * pl.splits * pl.rows * (c->head_dim + 2) * sizeof(float);
     return pl;
@@ -819,14 +827,7 @@ int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti
     const int wpg = pl.wpg, ng = pl.ng;
     dim3 grid(c->kv_heads, p.qtiles * pl.splits, a->num_seqs);
     const bool int8 = c->kind == TI_KV_INT8;
-    // Direct global -> LDS tile loads (bf16 dense cache, head_dim 128, pages of 2^k >= 16
-    // tokens) for two-wave key groups, the small grids: measured 13.8 -> 12.4 us at a
-    // 512-token prefill and 25.6 -> 23.3 us chunked, bit-identical; for four-wave groups
-    // (1024-3072 tokens) no change, so those keep the register-staged loads.
-    // TI_PREFILL_DL=0 never takes them, =1 also for four-wave groups (read per call).
-    const char *dl_env = getenv("TI_PREFILL_DL");
-    const int dl_force = dl_env ? atoi(dl_env) : -1;
-    const bool dl = dl_force == 1 || (dl_force != 0 && wpg == 2);
+    const bool dl = pl.dl;
     if (c->head_dim == 128) {
         if (int8) launch_prefill_d<128, true>(p, wpg, ng, dl, grid, s);
         else launch_prefill_d<128, false>(p, wpg, ng, dl, grid, s);

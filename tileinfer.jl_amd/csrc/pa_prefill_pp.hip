@@ -93,10 +93,10 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
     const int split = (int)blockIdx.y % p.splits;
     const int b = blockIdx.z;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? p.qsl[b + 1] - tok0 : p.nmax;
+    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
     const int t_first = qt * p.TQ;
     if (t_first >= nb) return;
-    const int start = p.positions[tok0], len = start + nb;
+    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
     const int t_last = min(t_first + p.TQ, nb) - 1;
     const int kend = p.causal ? start + t_last + 1 : len;
     const int nkt = (kend + KT - 1) / KT;
@@ -128,8 +128,7 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
     auto half_base = [&](int j) -> long long {
         const int kt = kt_lo + min(j, N - 1);
         const int pos = kt * KT + 16 * half;
-        const int idx = min(pos >> p.pshift, p.bt_stride - 1);
-        const int pg = page_of_s(bt, idx, p.num_pages);
+        const int pg = page_of_s(bt, pos >> p.pshift, p.bt_stride, p.num_pages);
         return (((long long)pg * p.Hk + h) * p.P + (pos & (p.P - 1))) * D;
     };
 

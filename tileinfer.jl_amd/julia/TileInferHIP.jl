@@ -85,10 +85,29 @@ function attention_args(out, q::ROCArray{T,3}, block_table, positions, scale, ca
                   ws === nothing ? 0 : sizeof(ws))
 end
 
+# A shape-only ti_attention_args for ti_attention_workspace_bytes: the query's dtype and
+# shape (one sequence of n tokens). The size query never dereferences a pointer, but the
+# argument check wants them non-null, so they are a fixed non-null placeholder.
+function workspace_query(q::ROCArray{T,3}) where {T}
+    D, heads, n = size(q)
+    nz = Ptr{Cvoid}(1)
+    AttentionArgs(dtype_code(T), heads, 1, n, n, 1, nz, nz, Ptr{Int32}(1), C_NULL, Ptr{Int32}(1),
+                  1.0f0, Int32(1), TI_PATH_AUTO, C_NULL, 0)
+end
+
+# The shape-only ti_kv_cache of a pool (dense ROCArray or either Int8Pages half).
+function workspace_cache(k_pages)
+    D, P, H, pages = size(k_pages)
+    nz = Ptr{Cvoid}(1)
+    k_pages isa Int8Pages ?
+        KVCache(TI_KV_INT8, D, P, H, pages, C_NULL, C_NULL, Ptr{Int8}(1), Ptr{Float32}(1), Ptr{Float32}(1)) :
+        KVCache(TI_KV_DENSE, D, P, H, pages, nz, nz, C_NULL, C_NULL, C_NULL)
+end
+
 # attention_workspace(::TileBackend, q, k_pages): src/ops/tile/attention.jl:351-352
 function TileInfer.attention_workspace(::HipBackend, q::ROCArray{T,3}, k_pages) where {T}
-    c = Ref(kv_cache(k_pages, k_pages isa Int8Pages ? k_pages : k_pages))
-    a = Ref(attention_args(q, q, q, q, 1, true, nothing))     # shapes only
+    c = Ref(workspace_cache(k_pages))
+    a = Ref(workspace_query(q))
     n = Ref{Csize_t}(0)
     check(ccall((:ti_attention_workspace_bytes, LIB), Cint,
                 (Ptr{AttentionArgs}, Ptr{KVCache}, Ptr{Csize_t}), a, c, n))
