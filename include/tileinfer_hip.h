@@ -137,6 +137,25 @@ int ti_attention_workspace_bytes(const ti_attention_args *args, const ti_kv_cach
  */
 int ti_attention(const ti_attention_args *args, const ti_kv_cache *cache, void *stream);
 
+/* Bytes of the static device scratch behind ti_attention_noalloc (per GPU). */
+#define TI_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * ti_attention without a caller workspace and without any allocation: split-KV partials
+ * go to a static device array of TI_NOALLOC_SCRATCH_BYTES per GPU (the library's own,
+ * held until the process ends). No counterpart in the reference: this is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). It calls no hipMalloc / hipFree and no allocating library routine.
+ * Same arguments, kernels and results as ti_attention with a sufficient workspace;
+ * args->workspace and args->workspace_bytes are ignored. Shapes whose workspace
+ * (ti_attention_workspace_bytes) exceeds the scratch are rejected with TI_ERR_WORKSPACE
+ * before anything is launched. Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (several streams, several host threads) race and must be serialized
+ * by the caller. Nothing in the scratch needs clearing between calls (every partial a
+ * launch reads is written by the same launch). `stream` must belong to the current device.
+ */
+int ti_attention_noalloc(const ti_attention_args *args, const ti_kv_cache *cache, void *stream);
+
 /*
  * Write keys and values of n tokens at 1-based slots, bit-exact copies (dense) or
  * quantized per (token, KV head) vector (INT8: q = floor(x 127/max|x| + 1/2),

@@ -155,3 +155,28 @@ def test_python_layer_rejects_host_tensors():
         ti.attention_(ti.HipBackend(), q, None, q, torch.zeros((2, 2, 4, 64), dtype=torch.bfloat16),
                       torch.zeros((2, 2, 4, 64), dtype=torch.bfloat16), torch.zeros(4, dtype=torch.int32),
                       torch.zeros(1, dtype=torch.int32), 0.1)
+
+
+def test_noalloc_validates_before_any_hip_call():
+    """ti_attention_noalloc checks arguments and its scratch limit on the host first, so
+    these return without a GPU: invalid arguments as ti_attention, and shapes whose
+    workspace exceeds TI_NOALLOC_SCRATCH_BYTES with TI_ERR_WORKSPACE."""
+    L = ti.load_library()
+    assert L.ti_attention_noalloc(ctypes.byref(_args(q_heads=30)), ctypes.byref(_cache()), None) == \
+        _lib.TI_ERR_INVALID_ARG
+    assert L.ti_attention_noalloc(None, ctypes.byref(_cache()), None) == _lib.TI_ERR_INVALID_ARG
+    assert L.ti_attention_noalloc(ctypes.byref(_args()), ctypes.byref(_cache(head_dim=96)), None) == \
+        _lib.TI_ERR_UNSUPPORTED
+    # the ping-pong kernel pinned on a 512-token prefill of one KV head with G = 8: 16
+    # work-groups, so 16 key splits of 4096 packed rows: 16 * 4096 * 130 * 4 B > 32 MiB
+    c = _cache(kv_heads=1)
+    a = _args(q_heads=8, num_seqs=1, max_query_len=512, total_tokens=512,
+              path=_lib.TI_PATH_PREFILL_PINGPONG)
+    st, need = ws(a, c)
+    assert st == _lib.TI_OK and need > _lib.NOALLOC_SCRATCH_BYTES
+    assert L.ti_attention_noalloc(ctypes.byref(a), ctypes.byref(c), None) == _lib.TI_ERR_WORKSPACE
+    # 256 tokens: half the rows, within the scratch (not launched here: no GPU)
+    a = _args(q_heads=8, num_seqs=1, max_query_len=256, total_tokens=256,
+              path=_lib.TI_PATH_PREFILL_PINGPONG)
+    st, need = ws(a, c)
+    assert st == _lib.TI_OK and 0 < need <= _lib.NOALLOC_SCRATCH_BYTES

@@ -1,8 +1,36 @@
 // C ABI of libtileinfer_hip: argument validation (host only, before any HIP call) and
 // dispatch to the kernels. See include/tileinfer_hip.h for the contract of each entry.
+#include <mutex>
+
 #include "common.hpp"
 
+// Device scratch of ti_attention_noalloc: split-KV partials live here instead of in a
+// caller's workspace. One copy per GPU, allocated when the library's code object is
+// loaded on that GPU and held until the process ends. In host code `scratch` only names
+// the symbol; its device address (per GPU) comes from hipGetSymbolAddress.
+static __device__ __align__(256) char scratch[TI_NOALLOC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void *scratch_ptr[MAX_DEVICES];   // device address of `scratch` on each GPU, once looked up
+
+// The current GPU's scratch address: looked up once per GPU (with that GPU current, on
+// its first no-alloc call), then cached. No allocation happens here.
+int device_scratch(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return TI_ERR_LAUNCH;
+    if (dev < 0 || dev >= MAX_DEVICES) return TI_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return TI_ERR_LAUNCH;
+        scratch_ptr[dev] = p;
+    }
+    *out = scratch_ptr[dev];
+    return TI_OK;
+}
 
 bool bad_cache(const ti_kv_cache *c) {
     if (!c) return true;
@@ -114,6 +142,25 @@ int ti_attention(const ti_attention_args *a, const ti_kv_cache *c, void *stream)
     const ti_decode_plan pl = ti_plan_decode(a, c);
     if (pl.bytes > 0 && (!a->workspace || a->workspace_bytes < pl.bytes)) return TI_ERR_WORKSPACE;
     return ti_launch_decode(a, c, pl, s);
+}
+
+int ti_attention_noalloc(const ti_attention_args *a, const ti_kv_cache *c, void *stream) {
+    // The same validation and the same plan as ti_attention; the plan's workspace (sized
+    // as ti_attention_workspace_bytes, which bounds every launch of these shapes) must fit
+    // the static scratch, else the call is rejected before any HIP call.
+    size_t need = 0;
+    int st = ti_attention_workspace_bytes(a, c, &need);
+    if (st) return st;
+    if (need > (size_t)TI_NOALLOC_SCRATCH_BYTES) return TI_ERR_WORKSPACE;
+    ti_attention_args local = *a;
+    local.workspace = nullptr;
+    local.workspace_bytes = 0;
+    if (need > 0) {
+        st = device_scratch(&local.workspace);
+        if (st) return st;
+        local.workspace_bytes = TI_NOALLOC_SCRATCH_BYTES;
+    }
+    return ti_attention(&local, c, stream);
 }
 
 int ti_store_kv(int dtype, const ti_kv_cache *c, const void *k, const void *v,

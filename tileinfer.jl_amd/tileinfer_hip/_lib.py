@@ -20,7 +20,8 @@ TI_KV_DENSE, TI_KV_INT8 = 0, 1
 
 # Every symbol include/tileinfer_hip.h declares.
 EXPORTS = ("ti_version", "ti_status_string", "ti_attention_workspace_bytes", "ti_attention",
-           "ti_store_kv", "ti_rmsnorm", "ti_rope", "ti_attention_inputs")
+           "ti_attention_noalloc", "ti_store_kv", "ti_rmsnorm", "ti_rope", "ti_attention_inputs")
+NOALLOC_SCRATCH_BYTES = 32 << 20   # TI_NOALLOC_SCRATCH_BYTES
 
 
 class KVCache(ctypes.Structure):
@@ -64,6 +65,8 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     L.ti_attention_workspace_bytes.argtypes = [P(AttentionArgs), P(KVCache), P(ctypes.c_size_t)]
     L.ti_attention.restype = i32
     L.ti_attention.argtypes = [P(AttentionArgs), P(KVCache), vp]
+    L.ti_attention_noalloc.restype = i32
+    L.ti_attention_noalloc.argtypes = [P(AttentionArgs), P(KVCache), vp]
     L.ti_store_kv.restype = i32
     L.ti_store_kv.argtypes = [i32, P(KVCache), vp, vp, vp, i32, vp]
     L.ti_rmsnorm.restype = i32
