@@ -54,7 +54,10 @@ typedef enum { TI_KV_DENSE = 0, TI_KV_INT8 = 1 } ti_kv_kind;
  *   PREFILL_DIRECT    four-wave kernel, direct global -> LDS tile loads (bf16 dense cache,
  *                     head_dim 128, pages of 2^k >= 16 tokens; otherwise staged)
  *   PREFILL_PINGPONG  eight-wave ping-pong kernel (bf16 dense cache, head_dim 128, pages
- *                     of 2^k >= 16 tokens, 256 % (q_heads / kv_heads) == 0) */
+ *                     of 2^k >= 16 tokens, 256 % (q_heads / kv_heads) == 0)
+ *   PREFILL_PAIRED    four-wave kernel with direct loads whose work-groups each take a
+ *                     heavy and a light 32-row q-tile of a causal step (direct-load shapes,
+ *                     32 % (q_heads / kv_heads) == 0, the shapes' unsplit two-wave plan) */
 typedef enum {
     TI_PATH_AUTO = 0,
     TI_PATH_DECODE = 1,
@@ -62,6 +65,7 @@ typedef enum {
     TI_PATH_PREFILL_STAGED = 3,
     TI_PATH_PREFILL_DIRECT = 4,
     TI_PATH_PREFILL_PINGPONG = 5,
+    TI_PATH_PREFILL_PAIRED = 6,
 } ti_path;
 
 /* One layer's KV cache: dense pools in the activations' type, or an INT8 layer

@@ -229,14 +229,17 @@ def test_workspace_errors(gpu):
 # (head_dim, heads, kv_heads, page_size, start, n, causal, batch)
 LOADER_CASES = [(128, 32, 8, 16, 0, 512, True, 1), (128, 32, 8, 16, 1024, 512, True, 1),
                 (128, 32, 8, 16, 4096, 16, True, 4), (128, 32, 8, 64, 300, 250, False, 1),
-                (128, 24, 8, 32, 77, 301, True, 1), (128, 32, 8, 16, 0, 2048, True, 1)]
+                (128, 24, 8, 32, 77, 301, True, 1), (128, 32, 8, 16, 0, 2048, True, 1),
+                # odd q-tile counts: the paired kernel's middle q-tile pairs with itself
+                (128, 32, 8, 16, 0, 200, True, 2), (128, 16, 8, 16, 37, 100, True, 3)]
 
 
 @pytest.mark.parametrize("case", LOADER_CASES, ids=str)
 def test_prefill_tile_loaders_bit_identical(gpu, case):
     """The four-wave prefill kernel's two tile loaders (register-staged loads + LDS stores,
     TI_PATH_PREFILL_STAGED; direct global -> LDS loads into swizzled rows,
-    TI_PATH_PREFILL_DIRECT) feed
+    TI_PATH_PREFILL_DIRECT; and the same with paired heavy / light q-tiles,
+    TI_PATH_PREFILL_PAIRED, where causal shapes allow it) feed
     the same operands to the same arithmetic: outputs must be bit-identical, and within
     the tolerances of the oracle."""
     D, H, KVH, P, start, n, causal, B = case
@@ -254,14 +257,15 @@ def test_prefill_tile_loaders_bit_identical(gpu, case):
     kd, vd = dev(kp, torch.bfloat16), dev(vp, torch.bfloat16)
     pos = torch.arange(start, L, dtype=torch.int32, device="cuda").repeat(B)
     outs = []
-    for path in (ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT):
+    for path in (ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT, ti.TI_PATH_PREFILL_PAIRED):
         ws = ti.attention_workspace(BE, qd, kd, num_seqs=B, max_query_len=n, path=path)
         out = torch.full_like(qd, float("nan"))
         ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(), pos, 1 / math.sqrt(D),
                             causal, max_query_len=n, path=path)
         outs.append(out)
     assert torch.equal(outs[0], outs[1])
-    got = outs[1].float().cpu().numpy()
+    assert torch.equal(outs[1], outs[2])
+    got = outs[2].float().cpu().numpy()
     for b in range(B):
         ref = orc.attention(q[b * n:(b + 1) * n], bts[b], start, 1 / math.sqrt(D), causal, kp, vp)
         assert float(np.max(np.abs(ref - got[b * n:(b + 1) * n]))) <= 2e-2

@@ -77,7 +77,8 @@ def test_random_shape(gpu, seed):
         # wherever its shape limits allow) and through both tile loaders of the four-wave
         # kernel (STAGED: register-staged loads; DIRECT: direct global -> LDS loads
         # wherever they apply)
-        paths += [ti.TI_PATH_PREFILL_PINGPONG, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT]
+        paths += [ti.TI_PATH_PREFILL_PINGPONG, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT,
+                  ti.TI_PATH_PREFILL_PAIRED]
     for path in paths:
         out = torch.full_like(qd, float("nan"))
         ws = ti.attention_workspace(BE, qd, k, path=path)

@@ -25,9 +25,16 @@
 //                    straight from the coalesced row loads).
 //                    O^T's lane layout keeps each lane on its own row, so the rescale by
 //                    alpha needs no shuffles.
-// INT8 keys and values are exact in bf16; a key's scale multiplies its scores and a
-// value's scale its probability (src/ops/quant.jl:56-72); queries are multiplied by the
-// keys' smoothing and rounded to bf16 (attention.jl:90-95).
+// INT8 (src/ops/quant.jl:56-72; attention.jl:68-95): a key's scale multiplies its scores
+// and a value's scale its probability; queries are multiplied by the keys' smoothing and
+// rounded to bf16 (attention.jl:90-95). Both products run on fp16 MFMAs whose int8
+// operands cost one byte permute per two values: with u = b ^ 0x80 (= b + 128), the fp16
+// bit pattern 0x6400 | u is exactly 1152 + b. The biases come off in fp32: each score
+// loses 1152 sum(q), each output row 1152 sum(p) (sum(p) from one more MFMA against a
+// tile of ones). A query row enters fp16 as its bf16 values times 2^e (its largest
+// magnitude scaled into [2^14, 2^15): exact, but for elements below 2^-28 of the largest),
+// and the scores are multiplied back by 2^-e; the probabilities (p <= 1: the running
+// max is exact for INT8) times the values' scales enter fp16 rounded to nearest.
 //
 // At the end the four waves merge their (m, l, O) through LDS and the group writes one
 // Float32 partial (acc[D], m, l) per packed row; the combine kernel merges the splits:
@@ -70,14 +77,41 @@ __device__ __forceinline__ s16x4 lds_tr16(const uint16_t *p) {
         (__attribute__((address_space(3))) s16x4 *)(__attribute__((address_space(3))) uint16_t *)p);
 }
 
-// 8 int8 -> 8 bf16 words (exact).
-__device__ __forceinline__ u32x4 i8x8_to_bf16(uint2 v) {
-    u32x4 r;
-    uint32_t a, b, c, d;
-    i8x4_to_bf16(v.x, a, b);
-    i8x4_to_bf16(v.y, c, d);
-    r[0] = a; r[1] = b; r[2] = c; r[3] = d;
-    return r;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// The fp16 bias of the int8 operands: 0x6400 | (b ^ 0x80) is 1152 + b exactly.
+constexpr float I8_BIAS = 1152.0f;
+
+// 8 int8 (two words) -> 8 fp16 of 1152 + b: one xor per word, one byte permute per pair
+// (bytes 0x64 from the first source, the biased bytes from the second).
+__device__ __forceinline__ u32x4 i8x8_to_f16b(uint32_t x, uint32_t y) {
+    const uint32_t tx = x ^ 0x80808080u, ty = y ^ 0x80808080u;
+    return (u32x4){__builtin_amdgcn_perm(0x64646464u, tx, 0x04010400u),
+                   __builtin_amdgcn_perm(0x64646464u, tx, 0x04030402u),
+                   __builtin_amdgcn_perm(0x64646464u, ty, 0x04010400u),
+                   __builtin_amdgcn_perm(0x64646464u, ty, 0x04030402u)};
+}
+
+// S^T += K Q^T on one 32-wide head-dim block: bf16, or fp16 for INT8 caches.
+template <bool INT8>
+__device__ __forceinline__ f32x4 qk_mfma(u32x4 k, u32x4 q, f32x4 c) {
+    if constexpr (INT8)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, k), __builtin_bit_cast(f16x8, q),
+                                                      c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k), as_bf16x8(q), c, 0, 0, 0);
+}
+
+// O^T += V^T P^T on one 16-wide head-dim tile: bf16, or fp16 for INT8 caches.
+template <bool INT8>
+__device__ __forceinline__ f32x4 pv_mfma(s16x4 v, s16x4 pt, f32x4 c) {
+    if constexpr (INT8)
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, v), __builtin_bit_cast(f16x4, pt),
+                                                     c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(v, pt, c, 0, 0, 0);
 }
 
 // One 16-key tile's raw loads, held in registers from issue to use (software pipeline).
@@ -224,39 +258,68 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     const int mask_from = p.causal ? start : len - 1;
 
     // Query operands (B of S^T = K Q^T): row rb*16 + r16, elements i*32 + kg*8 .. +8.
-    bf16x8 qreg[ROWB][NKB];
+    // INT8: fp16 of the bf16-rounded q * smooth times 2^e (see the header); qcorr is the
+    // row's 1152 sum(q 2^e) that comes off its scores, qsl the score multiplier
+    // scale * log2(e) * 2^-e.
+    u32x4 qreg[ROWB][NKB];
     int qpos[ROWB];
+    float qcorr[ROWB], qsl[ROWB];
 #pragma unroll
     for (int rb = 0; rb < ROWB; rb++) {
         const int r = row0 + rb * 16 + r16, t = r / p.G, g = r - t * p.G;
         const bool ok = r < p.M && t < nb;
         qpos[rb] = p.causal && ok ? start + t : len - 1;
         const uint16_t *qr = p.q + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
+        if constexpr (!INT8) {
 #pragma unroll
-        for (int i = 0; i < NKB; i++) {
-            const int d0 = i * 32 + kg * 8;
-            if (!ok) {
-                qreg[rb][i] = as_bf16x8((u32x4){0u, 0u, 0u, 0u});
-            } else if (!INT8) {
-                qreg[rb][i] = as_bf16x8(*reinterpret_cast<const u32x4 *>(qr + d0));
-            } else {
-                const u32x4 raw = *reinterpret_cast<const u32x4 *>(qr + d0);
+            for (int i = 0; i < NKB; i++)
+                qreg[rb][i] = ok ? *reinterpret_cast<const u32x4 *>(qr + i * 32 + kg * 8) : (u32x4){0u, 0u, 0u, 0u};
+        } else {
+            float qf[NKB][8], amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NKB; i++) {
+                const int d0 = i * 32 + kg * 8;
+                const u32x4 raw = ok ? *reinterpret_cast<const u32x4 *>(qr + d0) : (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    // bf16(q * smooth) (attention.jl:90-95), kept as float
+                    qf[i][2 * e] = bf2f(f2bf(__uint_as_float(raw[e] << 16) * p.smooth[d0 + 2 * e]));
+                    qf[i][2 * e + 1] = bf2f(f2bf(__uint_as_float(raw[e] & 0xffff0000u) * p.smooth[d0 + 2 * e + 1]));
+                    amax = fmaxf(amax, fmaxf(fabsf(qf[i][2 * e]), fabsf(qf[i][2 * e + 1])));
+                }
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 16));
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            // amax * 2^e in [2^14, 2^15): frexp gives amax = f 2^x with f in [0.5, 1)
+            const int e2 = amax > 0.0f ? 15 - __builtin_amdgcn_frexp_expf(amax) : 0;
+            float qs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NKB; i++) {
                 u32x4 wv;
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    wv[e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * p.smooth[d0 + 2 * e],
-                                        __uint_as_float(raw[e] & 0xffff0000u) * p.smooth[d0 + 2 * e + 1]);
-                qreg[rb][i] = as_bf16x8(wv);
+                for (int e = 0; e < 4; e++) {
+                    const f16x2 hv = __builtin_convertvector(
+                        ((f32x2){__builtin_ldexpf(qf[i][2 * e], e2), __builtin_ldexpf(qf[i][2 * e + 1], e2)}), f16x2);
+                    qs += (float)hv[0] + (float)hv[1];
+                    wv[e] = __builtin_bit_cast(uint32_t, hv);
+                }
+                qreg[rb][i] = wv;
             }
+            qs += __shfl_xor(qs, 16);
+            qs += __shfl_xor(qs, 32);
+            qcorr[rb] = I8_BIAS * qs;
+            qsl[rb] = __builtin_ldexpf(p.scale_log2, -e2);
         }
     }
 
     f32x4 o[ROWB][NDT];
+    f32x4 psum[ROWB];   // INT8: sum of the fp16 probabilities (every element: the row's)
     float m[ROWB], l[ROWB];
 #pragma unroll
     for (int rb = 0; rb < ROWB; rb++) {
         m[rb] = NEG_BIG;
         l[rb] = 0.0f;
+        psum[rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dt = 0; dt < NDT; dt++) o[rb][dt] = (f32x4){0.f, 0.f, 0.f, 0.f};
     }
@@ -265,36 +328,24 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     const int vc = lane % CPR, vg = lane / CPR;   // V load: chunk, key group
 
     auto compute = [&](const TileRegs<D, INT8> &t, int j) {
-        // ---- V rows -> row-major LDS tile (INT8 converted to bf16, exact) ----
+        // ---- V rows -> row-major LDS tile (INT8: biased fp16, exact) ----
         u32x4 vrows[KPL];
 #pragma unroll
-        for (int e = 0; e < KPL; e++) vrows[e] = INT8 ? i8x8_to_bf16(make_uint2(t.v[e][0], t.v[e][1])) : t.v[e];
+        for (int e = 0; e < KPL; e++) vrows[e] = INT8 ? i8x8_to_f16b(t.v[e][0], t.v[e][1]) : t.v[e];
         lds_fence();   // the previous tile's reads of myvt are done before overwriting
 #pragma unroll
         for (int e = 0; e < KPL; e++)
             *reinterpret_cast<u32x4 *>(myvt + (vg * KPL + e) * VROW + vc * 8) = vrows[e];
         // ---- S^T = K Q^T ----
-        bf16x8 kreg[NKB];
+        u32x4 kreg[NKB];
 #pragma unroll
-        for (int i = 0; i < NKB; i++) {
-            if (!INT8) {
-                kreg[i] = as_bf16x8(t.k[i]);
-            } else {
-                u32x4 wv;
-                uint32_t a0, a1, a2, a3;
-                i8x4_to_bf16(t.k[i][0], a0, a1);
-                i8x4_to_bf16(t.k[i][1], a2, a3);
-                wv[0] = a0; wv[1] = a1; wv[2] = a2; wv[3] = a3;
-                kreg[i] = as_bf16x8(wv);
-            }
-        }
+        for (int i = 0; i < NKB; i++) kreg[i] = INT8 ? i8x8_to_f16b(t.k[i][0], t.k[i][1]) : t.k[i];
         f32x4 sc[ROWB];
 #pragma unroll
         for (int rb = 0; rb < ROWB; rb++) {
             sc[rb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < NKB; i++)
-                sc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kreg[i], qreg[rb][i], sc[rb], 0, 0, 0);
+            for (int i = 0; i < NKB; i++) sc[rb] = qk_mfma<INT8>(kreg[i], qreg[rb][i], sc[rb]);
         }
         // Scales of this lane's 4 score keys (kg*4 + e), from the lanes that loaded them.
         float skk[4], svk[4];
@@ -308,7 +359,8 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
         // ---- online softmax + P^T operands ----
         // Lazy rescaling: m is a reference max that only moves when a tile's max exceeds
         // it by more than RESCALE_LOG2 (then p <= 2^RESCALE_LOG2, safe in bf16 and fp32);
-        // l and O always use the same reference, so the result is exact.
+        // l and O always use the same reference, so the result is exact. INT8 moves m
+        // with every larger max (p <= 1, so p times a value scale stays within fp16).
         const bool need_mask = j * 16 + 15 > mask_from;
         s16x4 pop[ROWB];
         float x[ROWB][4], mt[ROWB];
@@ -319,8 +371,8 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 float v = sc[rb][e];
-                if (INT8) v *= skk[e];
-                v *= p.scale_log2;
+                if (INT8) v = (v - qcorr[rb]) * skk[e] * qsl[rb];
+                else v *= p.scale_log2;
                 if (need_mask) {
                     const int kp = j * 16 + kg * 4 + e;
                     v = (kp <= qpos[rb] && kp < len) ? v : -INFINITY;
@@ -328,7 +380,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
                 x[rb][e] = v;
                 mt[rb] = fmaxf(mt[rb], v);
             }
-            grow |= mt[rb] > m[rb] + RESCALE_LOG2;
+            grow |= mt[rb] > m[rb] + (INT8 ? 0.0f : RESCALE_LOG2);
         }
         if (__any(grow)) {
 #pragma unroll
@@ -339,6 +391,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
                 const float alpha = fast_exp2(m[rb] - mn);
                 m[rb] = mn;
                 l[rb] *= alpha;
+                if (INT8) psum[rb] *= alpha;
 #pragma unroll
                 for (int dt = 0; dt < NDT; dt++) o[rb][dt] *= alpha;
             }
@@ -353,7 +406,17 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
                 if (INT8) pe[e] *= svk[e];
             }
             l[rb] += ps;
-            pop[rb] = __builtin_bit_cast(s16x4, (u32x2){pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3])});
+            if (INT8) {
+                const f16x2 h0 = __builtin_convertvector(((f32x2){pe[0], pe[1]}), f16x2);
+                const f16x2 h1 = __builtin_convertvector(((f32x2){pe[2], pe[3]}), f16x2);
+                pop[rb] = __builtin_bit_cast(s16x4, (u32x2){__builtin_bit_cast(uint32_t, h0),
+                                                            __builtin_bit_cast(uint32_t, h1)});
+                // the row's sum of these fp16 probabilities, for the values' bias
+                const s16x4 ones = __builtin_bit_cast(s16x4, (u32x2){0x3c003c00u, 0x3c003c00u});
+                psum[rb] = pv_mfma<true>(ones, pop[rb], psum[rb]);
+            } else {
+                pop[rb] = __builtin_bit_cast(s16x4, (u32x2){pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3])});
+            }
         }
         // ---- O^T += V^T P^T ----
         lds_fence();   // this tile's V^T is in LDS
@@ -361,8 +424,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
         for (int dt = 0; dt < NDT; dt++) {
             const s16x4 a = lds_tr16(myvt + (4 * kg + (r16 >> 2)) * VROW + dt * 16 + 4 * (r16 & 3));
 #pragma unroll
-            for (int rb = 0; rb < ROWB; rb++)
-                o[rb][dt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pop[rb], o[rb][dt], 0, 0, 0);
+            for (int rb = 0; rb < ROWB; rb++) o[rb][dt] = pv_mfma<INT8>(a, pop[rb], o[rb][dt]);
         }
     };
 
@@ -397,6 +459,14 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
             j += STRIDE;
             if (j >= j1) break;
         }
+    }
+
+    // INT8: the values' bias, 1152 times each row's sum of fp16 probabilities
+    if constexpr (INT8) {
+#pragma unroll
+        for (int rb = 0; rb < ROWB; rb++)
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) o[rb][dt] -= I8_BIAS * psum[rb];
     }
 
     // ---- merge the waves' states (same rows, disjoint keys) through LDS slabs ----

@@ -47,6 +47,7 @@ struct PrefillParams {
 };
 
 constexpr int KT = 32;                 // keys per LDS tile
+constexpr bool PAIR_BY_DEFAULT = true; // AUTO / PREFILL take paired q-tiles where they apply
 constexpr float RESCALE_LOG2 = 8.0f;   // lazy-rescale threshold (see the decode kernel)
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -274,9 +275,18 @@ __device__ __forceinline__ u32x2 lds_tr16(const uint16_t *p) {
 //   O^T += V^T P^T  2 x D/32 v_mfma_f32_32x32x16_bf16; B = P^T is the score registers
 //                   (keys 0-15, then 16-31), A = V^T built by ds_read_b64_tr_b16 from the
 //                   row-major V tile (two 8-B transposing reads per operand).
-template <int D, bool INT8, bool PG16, int WPG, int NG, bool DL>
+//
+// PAIR (causal, unsplit, direct loads, two waves per group): the two waves of a key group
+// own two different 32-row q-tiles instead of one 64-row q-tile: a heavy one from the end
+// of the step (wave 0 of the group) and a light one from its start (wave 1), q-tiles
+// qtiles - 1 - y and y of work-group y, so every work-group carries the same causal work
+// (the light tile's keys are the first tiles of the heavy one's: they share the LDS
+// tiles). Waves 0-3 are the groups' heavy waves, 4-7 the light ones, one of each per SIMD;
+// a light wave past its keys only issues its share of the tile loads.
+template <int D, bool INT8, bool PG16, int WPG, int NG, bool DL, bool PAIR = false>
 __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p) {
     static_assert(!DL || (!INT8 && PG16 && D == 128 && (WPG == 2 || WPG == 4)), "direct loads: bf16, D 128, 2^k pages");
+    static_assert(!PAIR || (DL && WPG == 2 && NG == 4), "paired q-tiles: direct loads, 2 x 4 waves");
     constexpr int NQB = D / 16;          // QK MFMAs (16 head-dim elements each)
     constexpr int NDB = D / 32;          // 32-row output blocks of O^T
     constexpr int GT = 64 * WPG;         // threads per key group
@@ -292,48 +302,32 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
-    const int grp = w / WPG, wl = w % WPG, gtid = threadIdx.x % GT;
+    const int grp = PAIR ? w % NG : w / WPG, wl = PAIR ? w / NG : w % WPG, gtid = threadIdx.x % GT;
     const int r32 = lane & 31, kg = lane >> 5;
     // Grid (Hk, qtiles, B): consecutive work-groups (spread round-robin over the 8 XCDs)
     // belong to different KV heads, so each head's K/V stays in one XCD's L2.
     const int h = blockIdx.x;
-    const int qt = p.qtiles - 1 - (int)blockIdx.y / p.splits;   // heaviest tiles first
-    const int split = (int)blockIdx.y % p.splits;
+    // PAIR: qt is the heavy q-tile (it bounds the work-group's keys), qtw this wave's.
+    const int qt = PAIR ? p.qtiles - 1 - (int)blockIdx.y : p.qtiles - 1 - (int)blockIdx.y / p.splits;   // heaviest tiles first
+    const int qt_light = PAIR ? (int)blockIdx.y : qt;
+    const int qtw = PAIR && wl == 1 ? qt_light : qt;
+    const int split = PAIR ? 0 : (int)blockIdx.y % p.splits;
     const int b = blockIdx.z;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
     const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
     const int t_first = qt * p.TQ;
-    if (t_first >= nb) return;
-    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
-    const int t_last = min(t_first + p.TQ, nb) - 1;
-    const int kend = p.causal ? start + t_last + 1 : len;
-    const int nkt = (kend + KT - 1) / KT;
-    // This work-group's split: key tiles [kt_lo, kt_hi) of the q-tile's nkt.
-    const int per = (nkt + p.splits - 1) / p.splits;
-    const int kt_lo = min(split * per, nkt), kt_hi = min(kt_lo + per, nkt);
-    const int steps = (kt_hi - kt_lo + NG - 1) / NG;       // same for every group
-    const size_t unit = ((size_t)b * p.Hk + h) * p.splits + split;
+    if (qt_light * p.TQ >= nb) return;
+    const int t_first_w = qtw * p.TQ;
     const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
-    Smem<D> &sm = smg[grp];
-    DlSmem &dsm = reinterpret_cast<DlSmem *>(smem_raw)[grp];
-    const int mask_from = p.causal ? start + t_first : len - 1;
-    if (steps == 0) {
-        // A split with no keys (short sequence): neutral partials (m = -big, l = 0, acc = 0)
-        // that the combine weights to zero.
-        constexpr int RPGW = 32 * WPG;
-        for (int idx = threadIdx.x; idx < RPGW * (D + 2); idx += 64 * WPG * NG) {
-            const int rr = idx / (D + 2), c = idx - rr * (D + 2);
-            const int ttl = rr / p.G, gg = rr - ttl * p.G, tt = t_first + ttl;
-            if (ttl < p.TQ && tt < nb)
-                p.part[(unit * p.M + (size_t)tt * p.G + gg) * (D + 2) + c] = c == D ? NEG_BIG : 0.0f;
-        }
-        return;
-    }
-
+    // Loads that do not depend on the step's positions go out first, so their latency
+    // overlaps the positions load: the queries and, when keys are not split, the page ids
+    // of the group's first tile (tile grp; re-fetched below in the rare case that the
+    // q-tile has fewer key tiles than groups).
     // This lane's query row (B operand of S^T = K Q^T): elements i*16 + kg*8 .. +8.
-    const int r = wl * 32 + r32, tl = r / p.G, g = r - tl * p.G, t = t_first + tl;
-    const bool row_ok = tl < p.TQ && t < nb;
-    const int qpos = p.causal && row_ok ? start + t : len - 1;
+    const int r = wl * 32 + r32;                    // the row's place in the group's slab
+    const int rw = PAIR ? r32 : r, tl = rw / p.G, g = rw - tl * p.G, t = t_first_w + tl;
+    // PAIR with an odd count of q-tiles: the middle one pairs with itself (its light wave idles)
+    const bool row_ok = tl < p.TQ && t < nb && !(PAIR && wl == 1 && qt_light == qt);
     bf16x8 qreg[NQB];
     {
         const uint16_t *qr = p.q + ((size_t)(tok0 + (row_ok ? t : 0)) * p.Hq + h * p.G + g) * D;
@@ -356,6 +350,39 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         }
     }
 
+    TilePages spec{};
+    if constexpr (DL) {
+        if (p.splits == 1) spec = tile_pages(p, bt, grp);
+    }
+    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
+    const int qpos = p.causal && row_ok ? start + t : len - 1;
+    const int t_last = min(t_first + p.TQ, nb) - 1;
+    const int kend = p.causal ? start + t_last + 1 : len;
+    // this wave's own keys (PAIR: the light wave's end before the work-group's)
+    const int kend_w = PAIR && p.causal ? start + min(t_first_w + p.TQ, nb) : kend;
+    const int kt_hi_w = (kend_w + KT - 1) / KT;
+    const int nkt = (kend + KT - 1) / KT;
+    // This work-group's split: key tiles [kt_lo, kt_hi) of the q-tile's nkt.
+    const int per = (nkt + p.splits - 1) / p.splits;
+    const int kt_lo = min(split * per, nkt), kt_hi = min(kt_lo + per, nkt);
+    const int steps = (kt_hi - kt_lo + NG - 1) / NG;       // same for every group
+    const size_t unit = ((size_t)b * p.Hk + h) * p.splits + split;
+    Smem<D> &sm = smg[grp];
+    DlSmem &dsm = reinterpret_cast<DlSmem *>(smem_raw)[grp];
+    const int mask_from = p.causal ? start + t_first_w : len - 1;
+    if (steps == 0) {
+        // A split with no keys (short sequence): neutral partials (m = -big, l = 0, acc = 0)
+        // that the combine weights to zero.
+        constexpr int RPGW = 32 * WPG;
+        for (int idx = threadIdx.x; idx < RPGW * (D + 2); idx += 64 * WPG * NG) {
+            const int rr = idx / (D + 2), c = idx - rr * (D + 2);
+            const int ttl = rr / p.G, gg = rr - ttl * p.G, tt = t_first + ttl;
+            if (ttl < p.TQ && tt < nb)
+                p.part[(unit * p.M + (size_t)tt * p.G + gg) * (D + 2) + c] = c == D ? NEG_BIG : 0.0f;
+        }
+        return;
+    }
+
     f32x16 o[NDB];
 #pragma unroll
     for (int db = 0; db < NDB; db++)
@@ -369,6 +396,13 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
 
     auto compute = [&](int kt, int buf, auto &&issue_loads) {
         if constexpr (!DL) issue_loads();
+        if constexpr (PAIR) {
+            // a light wave past its keys: its share of the next tile's loads only
+            if (kt >= kt_hi_w) {
+                issue_loads();
+                return;
+            }
+        }
         // One accumulation chain: dependent v_mfma_f32_32x32x16_bf16 issue back to back
         // (31 cycles each, measured), and a second chain would cost 16 VALU adds.
         f32x16 sc;
@@ -419,7 +453,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         // A tile past this group's keys (its last step) runs the score stage on whatever
         // the buffer holds, fully masked, so the next loads and the score MFMAs share one
         // scheduling region; its PV stage is skipped.
-        const bool valid = kt < kt_hi;
+        const bool valid = kt < (PAIR ? kt_hi_w : kt_hi);
         const bool need_mask = !valid || kt * KT + KT - 1 > mask_from;
         // INT8: the scales of this lane's 16 score keys, 8 q + 4 kg + (0..3) for q = 0..3,
         // as four 16-B reads per array
@@ -440,7 +474,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
             if constexpr (INT8) v *= skq[e >> 2][e & 3];
             if (need_mask) {
                 const int kpos = kt * KT + key;
-                v = (valid && kpos <= qpos && kpos < kend) ? v : -INFINITY;
+                v = (valid && kpos <= qpos && kpos < kend_w) ? v : -INFINITY;
             }
             x[e] = v;
             mt = fmaxf(mt, v);
@@ -545,8 +579,10 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
                 }
             }
         };
-        // page ids of the next tile to load, fetched one load ahead
-        TilePages pn = tile_pages(p, bt, min(tile_of(0), kt_hi - 1));
+        // page ids of the next tile to load, fetched one load ahead (the first tile's with
+        // the queries, before the positions, when keys are not split)
+        const int ft = min(tile_of(0), kt_hi - 1);
+        TilePages pn = p.splits == 1 && ft == grp ? spec : tile_pages(p, bt, ft);
         auto issue = [&](int i, int buf) {
             if (i < steps) {
                 dl_load(min(tile_of(i), kt_hi - 1), buf, pn);
@@ -624,7 +660,10 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
 #pragma unroll
         for (int it = 0; it < IT; it++) {
             const int item = threadIdx.x + it * NT, rr = item / (D / 4), d4 = (item % (D / 4)) * 4;
-            const int ttl = rr / p.G, gg = rr - ttl * p.G, tt = t_first + ttl;
+            // PAIR: slab rows 0-31 are the heavy q-tile's, 32-63 the light one's
+            const int wr = PAIR ? rr / 32 : 0, rl = PAIR ? rr % 32 : rr;
+            const int ttl = rl / p.G, gg = rl - ttl * p.G, tt = (PAIR && wr ? qt_light : qt) * p.TQ + ttl;
+            if (PAIR && wr == 1 && qt_light == qt) continue;
             float mx = NEG_BIG;
 #pragma unroll
             for (int gi = 0; gi < NG; gi++) mx = fmaxf(mx, ml[it][gi].x);
@@ -677,7 +716,10 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
 }
 
 template <int D, bool INT8, bool PG16, bool DL>
-void launch_prefill_w2(const PrefillParams &p, int ng, dim3 grid, hipStream_t s) {
+void launch_prefill_w2(const PrefillParams &p, int ng, dim3 grid, hipStream_t s, bool pair = false) {
+    if constexpr (DL) {
+        if (pair) return (void)(prefill_kernel<D, INT8, PG16, 2, 4, true, true><<<grid, 512, 0, s>>>(p));
+    }
     switch (ng) {
         case 1: prefill_kernel<D, INT8, PG16, 2, 1, DL><<<grid, 128, 0, s>>>(p); break;
         case 2: prefill_kernel<D, INT8, PG16, 2, 2, DL><<<grid, 256, 0, s>>>(p); break;
@@ -694,10 +736,10 @@ void launch_prefill_w4(const PrefillParams &p, int ng, dim3 grid, hipStream_t s)
 }
 
 template <int D, bool INT8, bool PG16>
-void launch_prefill_g(const PrefillParams &p, int wpg, int ng, bool dl, dim3 grid, hipStream_t s) {
+void launch_prefill_g(const PrefillParams &p, int wpg, int ng, bool dl, dim3 grid, hipStream_t s, bool pair) {
     if (wpg == 2) {
         if constexpr (!INT8 && PG16 && D == 128) {
-            if (dl) return launch_prefill_w2<D, INT8, PG16, true>(p, ng, grid, s);
+            if (dl) return launch_prefill_w2<D, INT8, PG16, true>(p, ng, grid, s, pair);
         }
         launch_prefill_w2<D, INT8, PG16, false>(p, ng, grid, s);
     } else {
@@ -709,9 +751,9 @@ void launch_prefill_g(const PrefillParams &p, int wpg, int ng, bool dl, dim3 gri
 }
 
 template <int D, bool INT8>
-void launch_prefill_d(const PrefillParams &p, int wpg, int ng, bool dl, dim3 grid, hipStream_t s) {
-    if (p.P % 16 == 0 && p.pshift >= 0) launch_prefill_g<D, INT8, true>(p, wpg, ng, dl, grid, s);
-    else launch_prefill_g<D, INT8, false>(p, wpg, ng, dl, grid, s);
+void launch_prefill_d(const PrefillParams &p, int wpg, int ng, bool dl, dim3 grid, hipStream_t s, bool pair) {
+    if (p.P % 16 == 0 && p.pshift >= 0) launch_prefill_g<D, INT8, true>(p, wpg, ng, dl, grid, s, pair);
+    else launch_prefill_g<D, INT8, false>(p, wpg, ng, dl, grid, s, false);
 }
 
 }  // namespace
@@ -749,6 +791,7 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     pl.pp = pp_ok && (a->path == TI_PATH_PREFILL_PINGPONG ||
                       ((a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO) && pp_wgs >= 512));
     pl.dl = 0;
+    pl.pair = 0;
     if (pl.pp) {
         // Key splits (forced runs on small grids) while work-groups are fewer than the
         // CUs and every split keeps at least 8 key tiles of the longest context the
@@ -788,8 +831,18 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     // (1024-3072 tokens) no change, so those keep the register-staged loads.
     const bool dl_ok = c->kind == TI_KV_DENSE && a->dtype == TI_BF16 && c->head_dim == 128 &&
                        c->page_size >= 16 && (c->page_size & (c->page_size - 1)) == 0;
-    pl.dl = dl_ok && (a->path == TI_PATH_PREFILL_DIRECT ||
+    pl.dl = dl_ok && (a->path == TI_PATH_PREFILL_DIRECT || a->path == TI_PATH_PREFILL_PAIRED ||
                       (a->path != TI_PATH_PREFILL_STAGED && pl.wpg == 2));
+    // Paired q-tiles (a heavy and a light 32-row q-tile per work-group, equal causal work
+    // per work-group) for the two-wave, four-group direct-load shape of causal steps
+    // without key splits; G must divide 32 (whole positions per 32-row q-tile).
+    pl.pair = pl.dl && a->causal && pl.wpg == 2 && pl.ng == 4 && pl.splits == 1 && 32 % G == 0 &&
+              (a->path == TI_PATH_PREFILL_PAIRED || ((a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO) &&
+                                                     PAIR_BY_DEFAULT));
+    if (pl.pair) {
+        pl.TQ = 32 / G;
+        pl.qtiles = (a->max_query_len + pl.TQ - 1) / pl.TQ;
+    }
     pl.rows = G * a->max_query_len;
     pl.bytes = pl.splits == 1 ? 0 : (size_t)pairs * pl.splits * pl.rows * (c->head_dim + 2) * sizeof(float);
     return pl;
@@ -825,15 +878,15 @@ int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti
     p.TQ = pl.TQ;
     p.qtiles = pl.qtiles;
     const int wpg = pl.wpg, ng = pl.ng;
-    dim3 grid(c->kv_heads, p.qtiles * pl.splits, a->num_seqs);
+    dim3 grid(c->kv_heads, pl.pair ? (p.qtiles + 1) / 2 : p.qtiles * pl.splits, a->num_seqs);
     const bool int8 = c->kind == TI_KV_INT8;
     const bool dl = pl.dl;
     if (c->head_dim == 128) {
-        if (int8) launch_prefill_d<128, true>(p, wpg, ng, dl, grid, s);
-        else launch_prefill_d<128, false>(p, wpg, ng, dl, grid, s);
+        if (int8) launch_prefill_d<128, true>(p, wpg, ng, dl, grid, s, false);
+        else launch_prefill_d<128, false>(p, wpg, ng, dl, grid, s, pl.pair);
     } else {
-        if (int8) launch_prefill_d<64, true>(p, wpg, ng, dl, grid, s);
-        else launch_prefill_d<64, false>(p, wpg, ng, dl, grid, s);
+        if (int8) launch_prefill_d<64, true>(p, wpg, ng, dl, grid, s, false);
+        else launch_prefill_d<64, false>(p, wpg, ng, dl, grid, s, false);
     }
     if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
     return pl.splits > 1 ? ti_launch_combine(a, c, pl.rows, pl.splits, s) : TI_OK;
