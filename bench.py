@@ -12,7 +12,8 @@ config as stated), prefill TFLOP/s, INT8-KV decode, speculative-verify and fused
 KV-write figures of the other BASELINE configs alongside, the roofline of the decode kernel and the CPU
 baseline (the oracle's Float32 op on the host cores, a bounded sample). The headline is
 timed call by call (HIP events around K steps); the other legs replay a HIP graph of 20
-captured calls, which removes host launch overhead from their microsecond-scale figures.
+captured calls, which removes host launch overhead from their microsecond-scale figures,
+after half a second of replays so that each leg is timed at steady state.
 """
 from __future__ import annotations
 
@@ -51,10 +52,11 @@ def time_calls(fn, iters, warmup):
     return start.elapsed_time(stop) / iters
 
 
-def time_graph(fn, calls=20, replays=5):
-    """Average ms per call with `calls` calls captured in one HIP graph and the graph
-    replayed `replays` times (after one warm replay): GPU time without host launch
-    overhead, as a graph-capturing runner sees it."""
+def time_graph(fn, calls=20, replays=10, settle_s=0.5):
+    """Average ms per call with `calls` calls captured in one HIP graph, replayed `replays`
+    times after the graph has been replayed for about `settle_s` seconds: GPU time without
+    host launch overhead, as a graph-capturing runner sees it, at steady state (a leg's
+    first fraction of a second runs up to 15 % slower while the GPU's clocks settle)."""
     import torch
     for i in range(3):
         fn(i)
@@ -65,6 +67,11 @@ def time_graph(fn, calls=20, replays=5):
             fn(i)
     g.replay()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < settle_s:
+        for _ in range(5):
+            g.replay()
+        torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(replays):
