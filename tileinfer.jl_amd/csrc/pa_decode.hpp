@@ -165,6 +165,10 @@ __device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodePara
         uint32_t vr[KPL];
 #pragma unroll
         for (int e = 0; e < KPL; e++) vr[e] = (uint32_t)min(vg * KPL + e, last);
+        // Values are streamed with non-temporal loads: each value row is read once per
+        // split, and keeping them out of the caches measured 8-10% faster on bf16 pages and
+        // 4% on INT8 pages. Keys keep normal loads (non-temporal keys measured 26% slower on
+        // INT8 pages).
         if (!INT8) {
             const uint16_t *kb = p.kp + r0 * D, *vb = p.vp + r0 * D;
 #pragma unroll
@@ -172,7 +176,7 @@ __device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodePara
                 t.k[i] = *reinterpret_cast<const u32x4 *>(kb + (kr * D + i * 32 + kg * 8));
 #pragma unroll
             for (int e = 0; e < KPL; e++)
-                t.v[e] = *reinterpret_cast<const u32x4 *>(vb + (vr[e] * D + vc * 8));
+                t.v[e] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vb + (vr[e] * D + vc * 8)));
         } else {
             const int8_t *kb = p.lq + r0 * D, *vb = p.lq + half_q + r0 * D;
 #pragma unroll
@@ -182,8 +186,8 @@ __device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodePara
             }
 #pragma unroll
             for (int e = 0; e < KPL; e++) {
-                const uint2 r = *reinterpret_cast<const uint2 *>(vb + (vr[e] * D + vc * 8));
-                t.v[e] = (u32x4){r.x, r.y, 0u, 0u};
+                const u32x2 r = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(vb + (vr[e] * D + vc * 8)));
+                t.v[e] = (u32x4){r[0], r[1], 0u, 0u};
             }
             const float *sb = p.ls + r0;
             t.sk = sb[kr];

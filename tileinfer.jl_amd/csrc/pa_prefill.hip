@@ -545,6 +545,9 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
             koff[u] = (uint32_t)(key * D + ((slot ^ key) * 8)) * 2u;
             voff[u] = (uint32_t)(key * D + ((slot ^ (4 * ksub)) * 8)) * 2u;
         }
+        // Value rows load with cache-policy bits 3 (sc0 sc1), keys with the default policy:
+        // measured 12% faster on decode-like verify steps (few queries per sequence, every
+        // row read once) and unchanged on long prompts, whose q-tiles re-read the rows.
         auto dl_load = [&](int kt, int buf, const TilePages &tp) {
             typedef __attribute__((address_space(3))) void *lds_ptr;
             const int pos0 = kt * KT, last = kend - 1 - pos0;   // >= 0 for every tile loaded
@@ -561,7 +564,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
                 for (int u = 0; u < NQ; u++) {
                     const int q4 = q0 + u;
                     __builtin_amdgcn_global_load_lds(kb + koff[u], (lds_ptr)(kd + q4 * 512), 16, 0, 0);
-                    __builtin_amdgcn_global_load_lds(vb + voff[u], (lds_ptr)(vd + q4 * 512), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds(vb + voff[u], (lds_ptr)(vd + q4 * 512), 16, 0, 3);
                 }
             } else {
                 // the step's last tile: keys past its end read the last key's row (finite
@@ -575,7 +578,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
                     const long long row = (kk >> 4 ? base1 : base0) + (kk & 15) * D;
                     const int kc = slot ^ (key & 15), vc = slot ^ (4 * (key & 3));
                     __builtin_amdgcn_global_load_lds(p.kp + row + kc * 8, (lds_ptr)(kd + q4 * 512), 16, 0, 0);
-                    __builtin_amdgcn_global_load_lds(p.vp + row + vc * 8, (lds_ptr)(vd + q4 * 512), 16, 0, 0);
+                    __builtin_amdgcn_global_load_lds(p.vp + row + vc * 8, (lds_ptr)(vd + q4 * 512), 16, 0, 3);
                 }
             }
         };
