@@ -66,8 +66,11 @@ def ws(a, c):
 
 def test_workspace_bytes_decode_and_prefill():
     st, n = ws(_args(), _cache())
-    # 4 seqs x 8 KV heads -> 8 splits (256 work-groups), 4 packed rows, (D + 2) floats
-    assert st == 0 and n == 4 * 8 * 8 * 4 * 130 * 4
+    # 4 seqs x 8 KV heads -> 8 splits (256 work-groups), 4 packed rows, (D + 2) floats,
+    # shared out by length (flat mode): a {first work-group, pieces} pair per sequence
+    assert st == 0 and n == 4 * 8 * 8 * 4 * 130 * 4 + 4 * 2 * 4
+    # one sequence: its splits are fixed, no table
+    assert ws(_args(num_seqs=1, total_tokens=1), _cache()) == (0, 1 * 8 * 16 * 4 * 130 * 4)
     # 32 seqs x 8 KV heads: one split per (sequence, KV head) writes the output directly
     assert ws(_args(num_seqs=32, total_tokens=32), _cache()) == (0, 0)
     st, n = ws(_args(max_query_len=512, total_tokens=2048), _cache())

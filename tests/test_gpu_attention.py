@@ -180,6 +180,67 @@ def test_batched_ragged(gpu, path):
         check(ref, got[qsl[b]:qsl[b + 1]], True)
 
 
+def _run_batch(g, starts, counts, use_qsl, KVH=8, H=32, D=128, P=16):
+    """One call over sequences at `starts` with `counts` query tokens each; returns
+    (q, kp, vp, bts, qsl, out). Without `use_qsl` every sequence has max(counts) tokens."""
+    nmax = max(counts)
+    pages = sum(-(-(s + n) // P) for s, n in zip(starts, counts)) + 3
+    perm = g.permutation(pages) + 1
+    width = max(-(-(s + n) // P) for s, n in zip(starts, counts)) + 2
+    bts = np.zeros((len(starts), width), np.int32)
+    off = 0
+    for b, (s, n) in enumerate(zip(starts, counts)):
+        used = -(-(s + n) // P)
+        bts[b, :used] = perm[off:off + used]
+        off += used
+    kp, vp = randn(g, pages, KVH, P, D, bf16=True), randn(g, pages, KVH, P, D, bf16=True)
+    q = randn(g, sum(counts), H, D, bf16=True)
+    qsl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    positions = np.concatenate([np.arange(s, s + n) for s, n in zip(starts, counts)]).astype(np.int32)
+    qd = dev(q, torch.bfloat16)
+    out = torch.zeros_like(qd)
+    kd, vd = dev(kp, torch.bfloat16), dev(vp, torch.bfloat16)
+    ws = ti.attention_workspace(BE, qd, kd, num_seqs=len(starts), max_query_len=nmax)
+    ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(),
+                        torch.from_numpy(positions).cuda(), 1 / math.sqrt(D), True,
+                        query_start_loc=torch.from_numpy(qsl).cuda() if use_qsl else None,
+                        max_query_len=nmax)
+    return q, kp, vp, bts, qsl, out.float().cpu().numpy()
+
+
+# Split batches of 2-64 sequences share their work-groups out by length: one long sequence
+# among short ones (most work-groups on one sequence), an empty sequence, 64 sequences
+# (the largest such batch) and 65 (one split count for all), multi-token steps through
+# query_start_loc and through the uniform layout.
+FLAT_CASES = {
+    "one_long": ([8000, 15, 16, 17], [1, 1, 1, 1], True),
+    "empty_and_multi": ([3000, 700, 0, 40], [3, 0, 5, 8], True),
+    "b64": (None, 64, True),     # with 2 KV heads (128 pairs: 2 splits each)
+    "b65": (None, 65, True),
+    "uniform_layout": ([100, 5000, 2000, 64, 900, 1], [2, 2, 2, 2, 2, 2], False),
+}
+
+
+@pytest.mark.parametrize("name", list(FLAT_CASES))
+def test_split_shares_by_length(gpu, name):
+    g = rng(950 + list(FLAT_CASES).index(name))
+    starts, counts, use_qsl = FLAT_CASES[name]
+    if starts is None:
+        B = counts
+        starts = [int(x) for x in g.integers(0, 3000, size=B)]
+        counts = [1] * B
+        q, kp, vp, bts, qsl, got = _run_batch(g, starts, counts, use_qsl, KVH=2, H=8)
+    else:
+        q, kp, vp, bts, qsl, got = _run_batch(g, starts, counts, use_qsl)
+    nmax = max(counts)
+    for b, (s, n) in enumerate(zip(starts, counts)):
+        if n == 0:
+            continue
+        lo = qsl[b] if use_qsl else b * nmax
+        ref = orc.attention(q[lo:lo + n], bts[b], s, 1 / math.sqrt(128), True, kp, vp)
+        check(ref, got[lo:lo + n], True)
+
+
 # (head_dim, heads, kv_heads, page_size, start, n, causal, block-table width in pages)
 SPLIT_CASES = [(128, 32, 8, 16, 0, 16, True, 512),      # most splits hold no keys
                (128, 32, 8, 16, 2048, 16, True, 160),   # the verify shape on a long prefix

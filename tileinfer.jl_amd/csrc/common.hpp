@@ -116,14 +116,18 @@ struct ti_decode_plan {
     int splits;      // split-KV work-groups per (sequence, KV head)
     int waves;       // waves per work-group (4 or 8)
     int rows;        // packed query rows G * max_query_len
+    int flat;        // > 0: work-groups per KV head shared out over the sequences by length
+    size_t meta;     // flat: byte offset of the per-sequence {first work-group, pieces} table
     size_t bytes;    // workspace bytes
 };
 ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c);
 int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_decode_plan &p,
                      hipStream_t s);
-// Merge split partials [B][Hk][splits][rows][D + 2] from a->workspace into a->out.
+// Merge split partials [B][Hk][splits][rows][D + 2] from a->workspace into a->out; flat
+// mode (flat work-groups per KV head): partials [Hk][flat][rows][D + 2], each sequence's
+// pieces located by the decode kernel's table at meta.
 int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows, int splits,
-                      hipStream_t s);
+                      hipStream_t s, int flat = 0, int *meta = nullptr);
 
 struct ti_prefill_plan {
     int pp;          // 1: the 8-wave ping-pong kernel (pa_prefill_pp.hip)

@@ -22,19 +22,29 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     const int t = r / p.G, g = r - t * p.G;
     if (t >= nb) return;
     const size_t stride = (size_t)p.M * (D + 2);
-    const float *base = p.part + ((size_t)b * p.Hk + h) * p.splits * stride + (size_t)r * (D + 2);
+    // flat mode: the sequence's pieces are partial slots lo .. lo + n - 1 of the KV head; a
+    // sequence of one piece had its output written by the decode kernel
+    int splits = p.splits;
+    size_t first = ((size_t)b * p.Hk + h) * p.splits;
+    if (p.flat) {
+        const int2 mt = *reinterpret_cast<const int2 *>(p.meta + 2 * b);
+        if (mt.y <= 1) return;
+        splits = mt.y;
+        first = (size_t)h * p.flat + mt.x;
+    }
+    const float *base = p.part + first * stride + (size_t)r * (D + 2);
     // Splits in batches of SB (2, 4, 8 or 16: the launch takes the smallest that holds all
     // splits): every load of a batch (m, l and the row) is issued before any arithmetic,
     // and batches merge online, so up to SB splits cost one round trip.
     float mx = NEG_BIG, lsum = 0.0f, acc[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) acc[k] = 0.0f;
-    for (int sp0 = 0; sp0 < p.splits; sp0 += SB) {
+    for (int sp0 = 0; sp0 < splits; sp0 += SB) {
         float2 ml[SB];
         float dv[SB][PER];
 #pragma unroll
         for (int j = 0; j < SB; j++) {
-            const float *src = base + min(sp0 + j, p.splits - 1) * stride;
+            const float *src = base + min(sp0 + j, splits - 1) * stride;
             ml[j] = *reinterpret_cast<const float2 *>(src + D);
 #pragma unroll
             for (int k = 0; k < PER; k++) dv[j][k] = src[lane + 64 * k];
@@ -42,7 +52,7 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
         float bm = mx;
 #pragma unroll
         for (int j = 0; j < SB; j++)
-            if (sp0 + j < p.splits) bm = fmaxf(bm, ml[j].x);
+            if (sp0 + j < splits) bm = fmaxf(bm, ml[j].x);
         const float alpha = fast_exp2(mx - bm);
         mx = bm;
         lsum *= alpha;
@@ -50,7 +60,7 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
         for (int k = 0; k < PER; k++) acc[k] *= alpha;
 #pragma unroll
         for (int j = 0; j < SB; j++) {
-            const float wgt = sp0 + j < p.splits ? fast_exp2(ml[j].x - mx) : 0.0f;
+            const float wgt = sp0 + j < splits ? fast_exp2(ml[j].x - mx) : 0.0f;
             lsum += ml[j].y * wgt;
 #pragma unroll
             for (int k = 0; k < PER; k++) acc[k] += dv[j][k] * wgt;
@@ -140,9 +150,19 @@ ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c) 
     }
     if (forced > 0) sp = forced;
     if ((forced_waves == 4 || forced_waves == 8) && pl.rows <= 32) nw = forced_waves;
+    // Split batches of 2-64 sequences share their work-groups out by length (flat mode):
+    // the same B x splits work-groups per KV head, cut in proportion to each sequence's
+    // keys (TI_DECODE_FLAT=0 turns it off, tuning only).
+    static const int flat_on = [] {
+        const char *e = getenv("TI_DECODE_FLAT");
+        return e ? atoi(e) : 1;
+    }();
+    pl.flat = flat_on && sp > 1 && a->num_seqs >= 2 && a->num_seqs <= 64 ? sp * a->num_seqs : 0;
     pl.splits = sp;
     pl.waves = nw;
     pl.bytes = sp == 1 ? 0 : (size_t)pairs * sp * pl.rows * (c->head_dim + 2) * sizeof(float);
+    pl.meta = pl.bytes;   // per-sequence {first work-group, pieces} after the partials
+    if (pl.flat) pl.bytes += (size_t)a->num_seqs * 2 * sizeof(int);
     return pl;
 }
 
@@ -160,6 +180,9 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
     p.qsl = a->query_start_loc;
     p.bt = a->block_tables;
     p.part = (float *)a->workspace;
+    p.meta = pl.flat ? reinterpret_cast<int *>((char *)a->workspace + pl.meta) : nullptr;
+    p.B = a->num_seqs;
+    p.flat = pl.flat;
     p.bt_stride = a->block_table_stride;
     p.num_pages = c->num_pages;
     p.P = c->page_size;
@@ -173,7 +196,7 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
     p.causal = a->causal;
     p.scale_log2 = a->scale * LOG2E;
     const int rowb = (pl.rows + 15) / 16;
-    dim3 grid(pl.splits, c->kv_heads, a->num_seqs);
+    const dim3 grid = pl.flat ? dim3(pl.flat, c->kv_heads, 1) : dim3(pl.splits, c->kv_heads, a->num_seqs);
     const bool int8 = c->kind == TI_KV_INT8;
     if (c->head_dim == 128) {
         if (int8) launch_decode_p<128, true>(p, rowb, pl.waves, grid, s);
@@ -183,14 +206,18 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
         else launch_decode_p<64, false>(p, rowb, pl.waves, grid, s);
     }
     if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
-    return pl.splits == 1 ? TI_OK : ti_launch_combine(a, c, pl.rows, pl.splits, s);
+    if (pl.splits == 1) return TI_OK;
+    // the combine batches its loads by the mean pieces per sequence
+    return ti_launch_combine(a, c, pl.rows, pl.flat ? pl.flat / a->num_seqs : pl.splits, s, pl.flat, p.meta);
 }
 
 int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows, int splits,
-                      hipStream_t s) {
+                      hipStream_t s, int flat, int *meta) {
     DecodeParams p{};
     p.out = (uint16_t *)a->out;
     p.part = (float *)a->workspace;
+    p.flat = flat;
+    p.meta = meta;
     p.qsl = a->query_start_loc;
     p.Hk = c->kv_heads;
     p.Hq = a->q_heads;

@@ -57,9 +57,53 @@ struct DecodeParams {
     const float *ls, *smooth;
     const int32_t *positions, *qsl, *bt;
     float *part;
+    int *meta;   // flat mode: per sequence {first work-group, pieces}, written by the decode kernel
     int bt_stride, num_pages, P, pshift, Hk, Hq, G, nmax, M, splits, causal;
+    int B, flat;   // flat: work-groups per KV head shared by all sequences (0: `splits` each)
     float scale_log2;
 };
+
+// Flat mode: the W = p.flat work-groups of a KV head are shared out over the B sequences
+// in proportion to their 16-key tiles: sequence i gets 1 + (its share of the other W - B),
+// the shares cut from the running tile total, so pieces of every sequence are about equally
+// long and a long sequence no longer sets the end of the launch. Work-group x belongs to the
+// sequence whose range [lo, lo + n) holds x. Computed by every wave from the sequences'
+// positions (one lane per sequence, B <= 64) with a wave prefix sum: no extra round trip
+// beyond the positions load that every work-group makes anyway. Results are wave-uniform.
+struct FlatPiece {
+    int b, lo, n, tok0, nb, start;
+};
+__device__ inline FlatPiece flat_piece(const DecodeParams &p, int x, int lane) {
+    int tok0 = 0, nb = 0, st = 0, nt = 0;
+    if (lane < p.B) {
+        tok0 = p.qsl ? p.qsl[lane] : lane * p.nmax;
+        nb = p.qsl ? min(p.qsl[lane + 1] - tok0, p.nmax) : p.nmax;
+        if (nb > 0) {
+            st = max(p.positions[tok0], 0);
+            nt = (st + nb + 15) >> 4;
+        }
+    }
+    int incl = nt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d);
+        if (lane >= d) incl += v;
+    }
+    const long long total = __shfl(incl, 63);
+    const long long extra = p.flat - p.B;
+    const int lo = lane + (total ? (int)((incl - nt) * extra / total) : 0);
+    const int hi = lane + 1 + (total ? (int)(incl * extra / total) : 0);
+    const unsigned long long m = __ballot(lane < p.B && lo <= x);
+    const int b = 63 - __builtin_clzll(m);   // lo grows with the lane; lane 0's lo is 0 <= x
+    FlatPiece f;
+    f.b = b;
+    f.lo = __builtin_amdgcn_readlane(lo, b);
+    f.n = __builtin_amdgcn_readlane(hi, b) - f.lo;
+    f.tok0 = __builtin_amdgcn_readlane(tok0, b);
+    f.nb = __builtin_amdgcn_readlane(nb, b);
+    f.start = __builtin_amdgcn_readlane(st, b);
+    return f;
+}
 
 // Per-wave V tile in LDS: [16 keys][D + 16] bf16, row-major. The row stride (an odd
 // multiple of 32 B) puts the 8 rows x 32 B that 32 lanes of a transposing read touch on
@@ -247,13 +291,33 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     // RS = 2: waves pair up on the same keys, wave w holding rows MP*(w%2) .. + MP.
     const int rslice = RS == 2 ? (w & 1) : 0, kw = RS == 2 ? (w >> 1) : w;
     const int row0 = rslice * MP;
-    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
-    if (nb <= 0) return;
-    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
+    const int h = blockIdx.y;
+    int s, b, nsp, tok0, nb, start;
+    size_t unit;   // this work-group's partial slot
+    if (p.flat) {
+        const FlatPiece f = flat_piece(p, blockIdx.x, lane);
+        b = f.b;
+        s = blockIdx.x - f.lo;
+        nsp = f.n;
+        tok0 = f.tok0;
+        nb = f.nb;
+        start = f.start;
+        unit = (size_t)h * p.flat + blockIdx.x;
+        if (h == 0 && s == 0 && threadIdx.x == 0) *reinterpret_cast<int2 *>(p.meta + 2 * b) = make_int2(f.lo, f.n);
+        if (nb <= 0) return;
+    } else {
+        s = blockIdx.x;
+        b = blockIdx.z;
+        nsp = p.splits;
+        tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
+        nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
+        if (nb <= 0) return;
+        start = max(p.positions[tok0], 0);   // a negative position reads as 0
+        unit = ((size_t)b * p.Hk + h) * p.splits + s;
+    }
+    const int len = start + nb;
     const int ntiles = (len + 15) >> 4;
-    const int per = (ntiles + p.splits - 1) / p.splits;
+    const int per = (ntiles + nsp - 1) / nsp;
     const int j0 = s * per, j1 = min(j0 + per, ntiles);
     const size_t half_q = (size_t)p.num_pages * p.Hk * p.P * D;
     const size_t half_s = (size_t)p.num_pages * p.Hk * p.P;
@@ -492,7 +556,6 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
         }
     }
     __syncthreads();
-    const size_t unit = ((size_t)b * p.Hk + h) * p.splits + s;
     for (int item = threadIdx.x; item < p.M * (D / 4); item += NW * 64) {
         const int r = item / (D / 4), d4 = (item % (D / 4)) * 4;
         const int rs = RS == 2 ? r / MP : 0, rr = r - rs * MP;   // row slice, row in slab
@@ -508,7 +571,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
             lsum += src[D + 1] * wgt;
             acc += *reinterpret_cast<const f32x4 *>(src + d4) * wgt;
         }
-        if (p.splits == 1) {
+        if (nsp == 1) {
             // One split: this group saw every key; normalize and write the output rows.
             const int t = r / p.G, g = r - t * p.G;
             if (t < nb) {
