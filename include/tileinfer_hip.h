@@ -47,7 +47,7 @@ typedef enum { TI_KV_DENSE = 0, TI_KV_INT8 = 1 } ti_kv_kind;
 /* Path selection for ti_attention. AUTO follows the reference's rule
  * (src/ops/tile/attention.jl:265, :351-352): split-KV decode for short steps, the prefill
  * kernel otherwise. PREFILL takes the prefill family and lets the library pick its
- * variant from host shapes; the last three pin one variant of it (for tests and tuning:
+ * variant from host shapes; the last five pin one variant of it (for tests and tuning:
  * every variant gives results within the same tolerances, and pinned variants that the
  * shapes do not allow fall back to the library's pick):
  *   PREFILL_STAGED    four-wave kernel, K/V tiles staged through registers into LDS
@@ -57,7 +57,9 @@ typedef enum { TI_KV_DENSE = 0, TI_KV_INT8 = 1 } ti_kv_kind;
  *                     of 2^k >= 16 tokens, 256 % (q_heads / kv_heads) == 0)
  *   PREFILL_PAIRED    four-wave kernel with direct loads whose work-groups each take a
  *                     heavy and a light 32-row q-tile of a causal step (direct-load shapes,
- *                     32 % (q_heads / kv_heads) == 0, the shapes' unsplit two-wave plan) */
+ *                     32 % (q_heads / kv_heads) == 0, the shapes' unsplit two-wave plan)
+ *   PREFILL_PAIRED16  the same paired work-groups on sixteen waves of 16 rows each (four
+ *                     per SIMD; the default where the paired plan applies) */
 typedef enum {
     TI_PATH_AUTO = 0,
     TI_PATH_DECODE = 1,
@@ -66,6 +68,7 @@ typedef enum {
     TI_PATH_PREFILL_DIRECT = 4,
     TI_PATH_PREFILL_PINGPONG = 5,
     TI_PATH_PREFILL_PAIRED = 6,
+    TI_PATH_PREFILL_PAIRED16 = 7,
 } ti_path;
 
 /* One layer's KV cache: dense pools in the activations' type, or an INT8 layer

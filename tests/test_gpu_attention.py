@@ -332,6 +332,41 @@ def test_prefill_tile_loaders_bit_identical(gpu, case):
         assert float(np.max(np.abs(ref - got[b * n:(b + 1) * n]))) <= 2e-2
 
 
+
+@pytest.mark.parametrize("case", LOADER_CASES, ids=str)
+def test_prefill_paired16(gpu, case):
+    """The paired work-groups on 16-row waves (TI_PATH_PREFILL_PAIRED16, AUTO's pick for the
+    paired shapes) against the oracle and the 32-row paired kernel: the same attention with
+    a different MFMA shape (16x16x32 instead of 32x32x16), so equal within the tolerances,
+    not bit for bit."""
+    D, H, KVH, P, start, n, causal, B = case
+    g = rng(1400 + n + start + B)
+    L = start + n
+    per = -(-L // P)
+    pages = B * per + 2
+    perm = g.permutation(pages) + 1
+    bts = np.zeros((B, per + 3), np.int32)
+    for b in range(B):
+        bts[b, :per] = perm[b * per:(b + 1) * per]
+    q = randn(g, B * n, H, D, bf16=True)
+    kp, vp = randn(g, pages, KVH, P, D, bf16=True), randn(g, pages, KVH, P, D, bf16=True)
+    qd = dev(q, torch.bfloat16)
+    kd, vd = dev(kp, torch.bfloat16), dev(vp, torch.bfloat16)
+    pos = torch.arange(start, L, dtype=torch.int32, device="cuda").repeat(B)
+    outs = []
+    for path in (ti.TI_PATH_PREFILL_PAIRED16, ti.TI_PATH_PREFILL_PAIRED, ti.TI_PATH_AUTO):
+        ws = ti.attention_workspace(BE, qd, kd, num_seqs=B, max_query_len=n, path=path)
+        out = torch.full_like(qd, float("nan"))
+        ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(), pos, 1 / math.sqrt(D),
+                            causal, max_query_len=n, path=path)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[2])                 # AUTO takes it
+    got = outs[0].float().cpu().numpy()
+    assert float(np.max(np.abs(got - outs[1].float().cpu().numpy()))) <= 2e-2
+    for b in range(B):
+        ref = orc.attention(q[b * n:(b + 1) * n], bts[b], start, 1 / math.sqrt(D), causal, kp, vp)
+        check(ref, got[b * n:(b + 1) * n], True)
+
 # (head_dim, heads, kv_heads, page_size, start, n, table width in pages, dtype)
 NARROW_CASES = [(128, 32, 8, 16, 200, 1, 5, "bf16"), (128, 32, 8, 16, 0, 300, 7, "bf16"),
                 (128, 32, 8, 48, 100, 5, 1, "bf16"), (128, 32, 8, 16, 90, 16, 2, "bf16"),

@@ -52,7 +52,8 @@ def _check(q, start, n, ref_fn, kd, vd, bt, paths):
 
 # (start, n): decode, a 512-token prefill on a cached prefix, the verify shape
 STEPS = [(L - 1, 1), (L - 512, 512), (L - 16, 16)]
-PATHS = [ti.TI_PATH_AUTO, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT, ti.TI_PATH_PREFILL_PAIRED]
+PATHS = [ti.TI_PATH_AUTO, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT, ti.TI_PATH_PREFILL_PAIRED,
+         ti.TI_PATH_PREFILL_PAIRED16]
 
 
 def test_bf16_pool_past_2_31_elements(gpu):

@@ -78,7 +78,7 @@ def test_random_shape(gpu, seed):
         # kernel (STAGED: register-staged loads; DIRECT: direct global -> LDS loads
         # wherever they apply)
         paths += [ti.TI_PATH_PREFILL_PINGPONG, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT,
-                  ti.TI_PATH_PREFILL_PAIRED]
+                  ti.TI_PATH_PREFILL_PAIRED, ti.TI_PATH_PREFILL_PAIRED16]
     for path in paths:
         out = torch.full_like(qd, float("nan"))
         ws = ti.attention_workspace(BE, qd, k, path=path)

@@ -63,7 +63,8 @@ int resolve_path(const ti_attention_args *a, const ti_kv_cache *c) {
         case TI_PATH_PREFILL_STAGED:
         case TI_PATH_PREFILL_DIRECT:
         case TI_PATH_PREFILL_PINGPONG:
-        case TI_PATH_PREFILL_PAIRED: return G <= 64 ? 2 : -TI_ERR_UNSUPPORTED;
+        case TI_PATH_PREFILL_PAIRED:
+        case TI_PATH_PREFILL_PAIRED16: return G <= 64 ? 2 : -TI_ERR_UNSUPPORTED;
         default: return -TI_ERR_INVALID_ARG;
     }
 }

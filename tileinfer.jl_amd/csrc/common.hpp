@@ -133,6 +133,7 @@ struct ti_prefill_plan {
     int pp;          // 1: the 8-wave ping-pong kernel (pa_prefill_pp.hip)
     int dl;          // 1: direct global -> LDS tile loads in the four-wave kernel
     int pair;        // 1: paired heavy / light 32-row q-tiles per work-group (TQ, qtiles per 32 rows)
+    int r16;         // 1 (with pair): the paired work-groups on 16-row waves (prefill16_kernel)
     int wpg;         // waves per key group (32 packed rows each)
     int ng;          // key groups per work-group
     int splits;      // key splits across work-groups (partials merged by the combine kernel)

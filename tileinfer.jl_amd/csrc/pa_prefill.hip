@@ -48,6 +48,7 @@ struct PrefillParams {
 
 constexpr int KT = 32;                 // keys per LDS tile
 constexpr bool PAIR_BY_DEFAULT = true; // AUTO / PREFILL take paired q-tiles where they apply
+constexpr bool R16_BY_DEFAULT = true;  // paired q-tiles on 16-row waves (prefill16_kernel)
 constexpr float RESCALE_LOG2 = 8.0f;   // lazy-rescale threshold (see the decode kernel)
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -718,6 +719,280 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         }
 }
 
+// One 16-byte-per-lane direct global -> LDS load issued from inline assembly (scalar base,
+// per-lane 32-bit byte offset; NT: cache-policy bits sc0 nt). The compiler does not see
+// its LDS write, so it adds no waits of its own before LDS reads of the other buffer; the
+// caller waits with an explicit vmcnt and a barrier before any wave reads the tile.
+// lds_addr is wave-uniform (it goes to M0).
+template <bool NT>
+__device__ __forceinline__ void lds_dma16(const void *base, uint32_t voff, uint32_t lds) {
+    // the base and the LDS address are wave-uniform: pin them in scalar registers
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    // (readfirstlane returns int: each half goes through uint32_t, never sign-extended)
+    const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+    const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+    const void *sbase = reinterpret_cast<const void *>((hi << 32) | lo);
+    const uint32_t lds_addr = (uint32_t)__builtin_amdgcn_readfirstlane(lds);
+    if (NT)
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc0 nt" ::"v"(voff), "s"(sbase), "s"(lds_addr)
+                     : "memory");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_addr)
+                     : "memory");
+}
+// The same from a per-lane 64-bit address (the step's last tile, whose rows are clamped per key).
+template <bool NT>
+__device__ __forceinline__ void lds_dma16_v(const void *gptr, uint32_t lds) {
+    const uint32_t lds_addr = (uint32_t)__builtin_amdgcn_readfirstlane(lds);
+    if (NT)
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc0 nt" ::"v"(gptr), "s"(lds_addr) : "memory");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory");
+}
+
+// Paired q-tiles on 16-row waves (bf16 dense cache, D = 128, pages of 2^k >= 16 tokens,
+// causal, no key splits). The work of the paired kernel above — work-group y holds the
+// heavy q-tile qtiles - 1 - y and the light q-tile y, four key groups walk the key tiles
+// through their own double-buffered LDS tiles and merge at the end — with each q-tile's 32
+// rows split over two waves of 16 rows: 16 waves of at most 128 VGPRs, four per SIMD.
+// Wave w is wave wl = w / 4 of key group w % 4 (wl 0, 1: heavy rows 0-15, 16-31; 2, 3:
+// light rows), so a SIMD holds one group's four waves: two heavy waves with independent
+// dependency chains on the same tiles, whose MFMAs and softmax interleave.
+// Per wave (lane l: row r16 = l % 16 of the wave, k-group kg = l / 16) and 32-key tile:
+//   S^T = K Q^T     2 x D/32 v_mfma_f32_16x16x32_bf16 (keys 0-15, 16-31); A = K rows from
+//                   LDS (16 B per lane), B = Q^T in registers; the lane holds its row's
+//                   scores of keys 4 kg + e and 16 + 4 kg + e, e < 4.
+//   softmax         exp2 domain, 8 scores per lane, two xor shuffles for the row max.
+//   O^T += V^T P^T  D/16 v_mfma_f32_16x16x32_bf16; B = P^T is the score registers (k-index
+//                   8 kg + j: key 4 kg + j, then 16 + 4 kg + j - 4), A = V^T from two 8-B
+//                   transposing reads (rows 4 kg .. + 3 and 16 + 4 kg .. + 3).
+// A step issues the next tile's loads first (into the other buffer, from inline assembly),
+// then reads this tile's keys, runs the score MFMAs and the softmax, and only then reads
+// the values, so key and value operands never occupy registers together.
+__global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
+    constexpr int D = 128, NG = 4, NQB = D / 32, NDB = D / 16;
+    constexpr int HW = 2, NQ = 2;        // direct loads: waves per 16-key page half, instructions per wave
+    constexpr int RPG = 64, MROW = D + 4;
+    constexpr int SMEM = (int)sizeof(DlSmem) * NG, MERGE = NG * RPG * MROW * 4;
+    __shared__ __attribute__((aligned(16))) char smem_raw[SMEM > MERGE ? SMEM : MERGE];
+    float *mslab = reinterpret_cast<float *>(smem_raw);
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = w % NG, wl = w / NG;
+    const bool light = wl >= 2;
+    const int r16 = lane & 15, kg = lane >> 4;
+    const int h = blockIdx.x;
+    const int qt = p.qtiles - 1 - (int)blockIdx.y, qt_light = blockIdx.y;
+    const int qtw = light ? qt_light : qt;
+    const int b = blockIdx.z;
+    const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
+    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;
+    const int t_first = qt * p.TQ;
+    if (qt_light * p.TQ >= nb) return;
+    const int t_first_w = qtw * p.TQ;
+    const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
+    // This lane's row: row rr of its q-tile (B operand of S^T: elements 32 i + 8 kg .. + 8).
+    const int rr = 16 * (wl & 1) + r16, tl = rr / p.G, g = rr - tl * p.G, t = t_first_w + tl;
+    const bool row_ok = tl < p.TQ && t < nb && !(light && qt_light == qt);
+    u32x4 qreg[NQB];
+    {
+        const uint16_t *qr = p.q + ((size_t)(tok0 + (row_ok ? t : 0)) * p.Hq + h * p.G + g) * D;
+#pragma unroll
+        for (int i = 0; i < NQB; i++)
+            qreg[i] = row_ok ? *reinterpret_cast<const u32x4 *>(qr + 32 * i + 8 * kg) : (u32x4){0u, 0u, 0u, 0u};
+    }
+    const TilePages spec = tile_pages(p, bt, grp);   // before the positions: tile grp's pages
+    const int start = max(p.positions[tok0], 0), len = start + nb;
+    const int qpos = p.causal && row_ok ? start + t : len - 1;
+    const int t_last = min(t_first + p.TQ, nb) - 1;
+    const int kend = p.causal ? start + t_last + 1 : len;
+    const int kend_w = light && p.causal ? start + min(t_first_w + p.TQ, nb) : kend;
+    const int kt_hi_w = (kend_w + KT - 1) / KT;
+    const int nkt = (kend + KT - 1) / KT;
+    const int steps = (nkt + NG - 1) / NG;
+    const int mask_from = p.causal ? start + t_first_w : len - 1;
+    DlSmem &dsm = reinterpret_cast<DlSmem *>(smem_raw)[grp];
+
+    f32x4 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; db++) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m = NEG_BIG, l = 0.0f;
+    // transposing V reads: 16-lane group kg reads rows 4 kg + r16 / 4 (and + 16), columns
+    // 4 (r16 % 4) .. + 3 of each 16-column block; rows of one lane share key % 4
+    const int vrow = 4 * kg + (r16 >> 2), vsw = 4 * (r16 >> 2);
+    const int vc_lo = (r16 & 3) >> 1, vc_off = 4 * (r16 & 1);
+
+    // direct loads: wave wl issues instructions q0, q0 + 1 of page half dx (instruction q4
+    // writes keys 4 q4 + lane / 16 of the half, 16-B slot lane % 16)
+    const int dx = wl / HW, q0 = NQ * (wl % HW);
+    const int ksub = lane >> 4, slot = lane & 15;
+    uint32_t koff[NQ], voff[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; u++) {
+        const int key = 4 * (q0 + u) + ksub;
+        koff[u] = (uint32_t)(key * D + ((slot ^ key) * 8)) * 2u;
+        voff[u] = (uint32_t)(key * D + ((slot ^ (4 * ksub)) * 8)) * 2u;
+    }
+    auto dl_load = [&](int kt, int buf, const TilePages &tp) {
+        const int pos0 = kt * KT, last = kend - 1 - pos0;   // >= 0 for every tile loaded
+        const uint32_t kd = (uint32_t)(uintptr_t)&dsm.k[buf][dx * 2048];
+        const uint32_t vd = (uint32_t)(uintptr_t)&dsm.v[buf][dx * 2048];
+        if (last >= KT - 1) {
+            const int pg = dx ? tp.pg[1] : tp.pg[0];
+            const long long base = (((long long)pg * p.Hk + h) * p.P + ((pos0 + 16 * dx) & (p.P - 1))) * D;
+            const uint16_t *kb = p.kp + base, *vb = p.vp + base;
+#pragma unroll
+            for (int u = 0; u < NQ; u++) {
+                lds_dma16<false>(kb, koff[u], kd + (q0 + u) * 1024);
+                lds_dma16<true>(vb, voff[u], vd + (q0 + u) * 1024);
+            }
+        } else {
+            const long long base0 = (((long long)tp.pg[0] * p.Hk + h) * p.P + (pos0 & (p.P - 1))) * D;
+            const long long base1 = (((long long)tp.pg[1] * p.Hk + h) * p.P + ((pos0 + 16) & (p.P - 1))) * D;
+#pragma unroll
+            for (int u = 0; u < NQ; u++) {
+                const int q4 = q0 + u;
+                const int key = 16 * dx + 4 * q4 + ksub, kk = min(key, last);
+                const long long row = (kk >> 4 ? base1 : base0) + (kk & 15) * D;
+                const int kc = slot ^ (key & 15), vc = slot ^ (4 * (key & 3));
+                lds_dma16_v<false>(p.kp + row + kc * 8, kd + q4 * 1024);
+                lds_dma16_v<true>(p.vp + row + vc * 8, vd + q4 * 1024);
+            }
+        }
+    };
+
+    auto compute = [&](int kt, int buf, auto &&issue_loads) {
+        issue_loads();
+        if (kt >= kt_hi_w) return;   // past this wave's keys (a light wave, or the group's last step)
+        const uint16_t *kt_lds = &dsm.k[buf][0];
+        f32x4 sc[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++) {
+            u32x4 ka[NQB];
+            const uint16_t *krow = kt_lds + (16 * kb + r16) * D;
+#pragma unroll
+            for (int i = 0; i < NQB; i++) ka[i] = *reinterpret_cast<const u32x4 *>(krow + (((4 * i + kg) ^ r16) * 8));
+            sc[kb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < NQB; i++)
+                sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[i]), as_bf16x8(qreg[i]), sc[kb], 0, 0, 0);
+        }
+        const bool need_mask = kt * KT + KT - 1 > mask_from;
+        float x[8], mt = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float v = sc[e >> 2][e & 3];
+            if (need_mask) {
+                const int kpos = kt * KT + 16 * (e >> 2) + 4 * kg + (e & 3);
+                v = (kpos <= qpos && kpos < kend_w) ? v : -INFINITY;
+            }
+            x[e] = v;
+            mt = fmaxf(mt, v);
+        }
+        mt *= p.scale_log2;
+        if (__any(mt > m + RESCALE_LOG2)) {
+            mt = fmaxf(mt, __shfl_xor(mt, 16));
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float mn = fmaxf(m, mt);
+            const float alpha = fast_exp2(m - mn);
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; db++) o[db] *= alpha;
+        }
+        float pe[8], ps = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            pe[e] = fast_exp2(__builtin_fmaf(x[e], p.scale_log2, -m));
+            ps += pe[e];
+        }
+        l += ps;
+        const u32x4 pb = {pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3]), pack_bf16x2(pe[4], pe[5]),
+                          pack_bf16x2(pe[6], pe[7])};
+        const uint16_t *vt = &dsm.v[buf][0];
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+            const int col = ((2 * db + vc_lo) ^ vsw) * 8 + vc_off;
+            const u32x2 lo = lds_tr16(vt + vrow * D + col);
+            const u32x2 hi = lds_tr16(vt + (vrow + 16) * D + col);
+            o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8((u32x4){lo[0], lo[1], hi[0], hi[1]}),
+                                                            as_bf16x8(pb), o[db], 0, 0, 0);
+        }
+    };
+
+    auto tile_of = [&](int i) { return grp + NG * i; };
+    const int ft = min(tile_of(0), nkt - 1);
+    TilePages pn = ft == grp ? spec : tile_pages(p, bt, ft);
+    auto issue = [&](int i, int buf) {
+        if (i < steps) {
+            dl_load(min(tile_of(i), nkt - 1), buf, pn);
+            pn = tile_pages(p, bt, min(tile_of(i + 1), nkt - 1));
+        }
+    };
+    issue(0, 0);
+    for (int i = 0; i < steps; i += 2) {
+        wait_direct_loads();
+        __syncthreads();
+        compute(tile_of(i), 0, [&] { issue(i + 1, 1); });
+        if (i + 1 >= steps) break;
+        wait_direct_loads();
+        __syncthreads();
+        compute(tile_of(i + 1), 1, [&] { issue(i + 2, 0); });
+    }
+    __syncthreads();   // every wave is done with the tiles before the merge reuses the LDS
+
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    // Merge the groups' states: slab rows 0-31 hold the heavy q-tile's rows, 32-63 the light one's.
+    {
+        float *my = mslab + ((size_t)grp * RPG + 32 * (wl >> 1) + rr) * MROW;
+#pragma unroll
+        for (int db = 0; db < NDB; db++) *reinterpret_cast<f32x4 *>(my + 16 * db + 4 * kg) = o[db];
+        if (kg == 0) {
+            my[D] = m;
+            my[D + 1] = l;
+        }
+    }
+    __syncthreads();
+    constexpr int NT = 1024, IT = RPG * (D / 4) / NT;
+    float2 ml[IT][NG];
+    f32x4 dv[IT][NG];
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int item = threadIdx.x + it * NT, sr = item / (D / 4), d4 = (item % (D / 4)) * 4;
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            const float *src = mslab + ((size_t)gi * RPG + sr) * MROW;
+            ml[it][gi] = *reinterpret_cast<const float2 *>(src + D);
+            dv[it][gi] = *reinterpret_cast<const f32x4 *>(src + d4);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int item = threadIdx.x + it * NT, sr = item / (D / 4), d4 = (item % (D / 4)) * 4;
+        const int wr = sr / 32, rl = sr % 32;
+        const int ttl = rl / p.G, gg = rl - ttl * p.G, tt = (wr ? qt_light : qt) * p.TQ + ttl;
+        if (wr == 1 && qt_light == qt) continue;
+        float mx = NEG_BIG;
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) mx = fmaxf(mx, ml[it][gi].x);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        float lsum = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < NG; gi++) {
+            const float wgt = fast_exp2(ml[it][gi].x - mx);
+            lsum += ml[it][gi].y * wgt;
+            acc += dv[it][gi] * wgt;
+        }
+        if (ttl >= p.TQ || tt >= nb) continue;
+        const float inv = 1.0f / lsum;
+        uint16_t *orow = p.out + ((size_t)(tok0 + tt) * p.Hq + h * p.G + gg) * D + d4;
+        *reinterpret_cast<u32x2 *>(orow) = (u32x2){pack_bf16x2(acc[0] * inv, acc[1] * inv),
+                                                   pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+    }
+}
+
 template <int D, bool INT8, bool PG16, bool DL>
 void launch_prefill_w2(const PrefillParams &p, int ng, dim3 grid, hipStream_t s, bool pair = false) {
     if constexpr (DL) {
@@ -795,6 +1070,7 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
                       ((a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO) && pp_wgs >= 512));
     pl.dl = 0;
     pl.pair = 0;
+    pl.r16 = 0;
     if (pl.pp) {
         // Key splits (forced runs on small grids) while work-groups are fewer than the
         // CUs and every split keeps at least 8 key tiles of the longest context the
@@ -835,13 +1111,19 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     const bool dl_ok = c->kind == TI_KV_DENSE && a->dtype == TI_BF16 && c->head_dim == 128 &&
                        c->page_size >= 16 && (c->page_size & (c->page_size - 1)) == 0;
     pl.dl = dl_ok && (a->path == TI_PATH_PREFILL_DIRECT || a->path == TI_PATH_PREFILL_PAIRED ||
+                      a->path == TI_PATH_PREFILL_PAIRED16 ||
                       (a->path != TI_PATH_PREFILL_STAGED && pl.wpg == 2));
     // Paired q-tiles (a heavy and a light 32-row q-tile per work-group, equal causal work
     // per work-group) for the two-wave, four-group direct-load shape of causal steps
     // without key splits; G must divide 32 (whole positions per 32-row q-tile).
     pl.pair = pl.dl && a->causal && pl.wpg == 2 && pl.ng == 4 && pl.splits == 1 && 32 % G == 0 &&
-              (a->path == TI_PATH_PREFILL_PAIRED || ((a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO) &&
+              (a->path == TI_PATH_PREFILL_PAIRED || a->path == TI_PATH_PREFILL_PAIRED16 ||
+               ((a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO) &&
                                                      PAIR_BY_DEFAULT));
+    // The paired work-groups on 16-row waves (prefill16_kernel) unless the 32-row paired
+    // kernel is pinned: measured 11.4 -> 10.4 us at a 512-token prefill and 22.0 -> 19.7 us
+    // chunked (512 on 1024), same process.
+    pl.r16 = pl.pair && a->path != TI_PATH_PREFILL_PAIRED && (a->path == TI_PATH_PREFILL_PAIRED16 || R16_BY_DEFAULT);
     if (pl.pair) {
         pl.TQ = 32 / G;
         pl.qtiles = (a->max_query_len + pl.TQ - 1) / pl.TQ;
@@ -882,6 +1164,10 @@ int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti
     p.qtiles = pl.qtiles;
     const int wpg = pl.wpg, ng = pl.ng;
     dim3 grid(c->kv_heads, pl.pair ? (p.qtiles + 1) / 2 : p.qtiles * pl.splits, a->num_seqs);
+    if (pl.r16) {
+        prefill16_kernel<<<grid, 1024, 0, s>>>(p);
+        return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
+    }
     const bool int8 = c->kind == TI_KV_INT8;
     const bool dl = pl.dl;
     if (c->head_dim == 128) {

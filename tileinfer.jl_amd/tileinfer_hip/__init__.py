@@ -5,7 +5,7 @@ Host-side mirror of the reference's op interface (src/ops/interface.jl) and KV l
 """
 from ._lib import (ArgumentError, TileInferError, WorkspaceError, TI_PATH_AUTO, TI_PATH_DECODE,
                    TI_PATH_PREFILL, TI_PATH_PREFILL_STAGED, TI_PATH_PREFILL_DIRECT,
-                   TI_PATH_PREFILL_PINGPONG, TI_PATH_PREFILL_PAIRED, EXPORTS, LIB_PATH, load as load_library)
+                   TI_PATH_PREFILL_PINGPONG, TI_PATH_PREFILL_PAIRED, TI_PATH_PREFILL_PAIRED16, EXPORTS, LIB_PATH, load as load_library)
 from .backend import (HipBackend, attention, attention_, attention_inputs_, attention_workspace,
                       has_kernel, kv_cache_struct, paged_attention_, rmsnorm, rmsnorm_, rope, rope_, store_kv_,
                       supports_graphs, workspace_bytes)

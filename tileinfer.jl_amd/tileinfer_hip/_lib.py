@@ -16,7 +16,7 @@ TI_OK, TI_ERR_INVALID_ARG, TI_ERR_UNSUPPORTED, TI_ERR_WORKSPACE, TI_ERR_LAUNCH =
 TI_F32, TI_BF16 = 0, 1
 TI_KV_DENSE, TI_KV_INT8 = 0, 1
 (TI_PATH_AUTO, TI_PATH_DECODE, TI_PATH_PREFILL, TI_PATH_PREFILL_STAGED, TI_PATH_PREFILL_DIRECT,
- TI_PATH_PREFILL_PINGPONG, TI_PATH_PREFILL_PAIRED) = range(7)
+ TI_PATH_PREFILL_PINGPONG, TI_PATH_PREFILL_PAIRED, TI_PATH_PREFILL_PAIRED16) = range(8)
 
 # Every symbol include/tileinfer_hip.h declares.
 EXPORTS = ("ti_version", "ti_status_string", "ti_attention_workspace_bytes", "ti_attention",
