@@ -819,8 +819,11 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     for (int db = 0; db < NDB; db++) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
     float m = NEG_BIG, l = 0.0f;
     // transposing V reads: 16-lane group kg reads rows 4 kg + r16 / 4 (and + 16), columns
-    // 4 (r16 % 4) .. + 3 of each 16-column block; rows of one lane share key % 4
-    const int vrow = 4 * kg + (r16 >> 2), vsw = 4 * (r16 >> 2);
+    // 4 (r16 % 4) .. + 3 of each 16-column block. Value rows are swizzled by their key:
+    // 16-B chunk c sits in slot c ^ 4 (key % 4) ^ 2 ((key / 4) % 2), so the four rows of one
+    // lane group fall in distinct 32-B windows and groups kg, kg + 1 (rows 4 apart) in the
+    // other half of the banks (bank-conflict cycles 1.33 M -> 4 K per chunked-prefill launch).
+    const int vrow = 4 * kg + (r16 >> 2), vsw = 4 * (r16 >> 2) ^ 2 * (kg & 1);
     const int vc_lo = (r16 & 3) >> 1, vc_off = 4 * (r16 & 1);
 
     // direct loads: wave wl issues instructions q0, q0 + 1 of page half dx (instruction q4
@@ -832,7 +835,7 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     for (int u = 0; u < NQ; u++) {
         const int key = 4 * (q0 + u) + ksub;
         koff[u] = (uint32_t)(key * D + ((slot ^ key) * 8)) * 2u;
-        voff[u] = (uint32_t)(key * D + ((slot ^ (4 * ksub)) * 8)) * 2u;
+        voff[u] = (uint32_t)(key * D + ((slot ^ (4 * (key & 3)) ^ (2 * ((key >> 2) & 1))) * 8)) * 2u;
     }
     auto dl_load = [&](int kt, int buf, const TilePages &tp) {
         const int pos0 = kt * KT, last = kend - 1 - pos0;   // >= 0 for every tile loaded
@@ -855,7 +858,7 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
                 const int q4 = q0 + u;
                 const int key = 16 * dx + 4 * q4 + ksub, kk = min(key, last);
                 const long long row = (kk >> 4 ? base1 : base0) + (kk & 15) * D;
-                const int kc = slot ^ (key & 15), vc = slot ^ (4 * (key & 3));
+                const int kc = slot ^ (key & 15), vc = slot ^ (4 * (key & 3)) ^ (2 * ((key >> 2) & 1));
                 lds_dma16_v<false>(p.kp + row + kc * 8, kd + q4 * 1024);
                 lds_dma16_v<true>(p.vp + row + vc * 8, vd + q4 * 1024);
             }
