@@ -333,12 +333,20 @@ def test_prefill_tile_loaders_bit_identical(gpu, case):
 
 
 
-@pytest.mark.parametrize("case", LOADER_CASES, ids=str)
+# Shapes on which AUTO takes the 16-row paired kernel: causal, unsplit, at most 512 pairs of
+# q-tiles (start, n, B); the other LOADER_CASES pin it where AUTO picks another kernel.
+PAIRED16_AUTO = {(0, 512, 1), (1024, 512, 1), (0, 200, 2), (0, 1024, 1)}
+
+
+@pytest.mark.parametrize("case", LOADER_CASES + [(128, 32, 8, 16, 0, 1024, True, 1)], ids=str)
 def test_prefill_paired16(gpu, case):
-    """The paired work-groups on 16-row waves (TI_PATH_PREFILL_PAIRED16, AUTO's pick for the
-    paired shapes) against the oracle and the 32-row paired kernel: the same attention with
-    a different MFMA shape (16x16x32 instead of 32x32x16), so equal within the tolerances,
-    not bit for bit."""
+    """The paired work-groups on 16-row waves (TI_PATH_PREFILL_PAIRED16, AUTO's pick for
+    causal steps of up to 512 pairs of q-tiles) against the oracle and the 32-row paired
+    kernel: the same attention with a different MFMA shape (16x16x32 instead of 32x32x16),
+    so equal within the tolerances, not bit for bit. The reference's ulp bound is stated for
+    its shapes (n <= 512); at 1024 new tokens every prefill variant gives the same 5.6 ulps
+    on this seed (the bf16 probabilities of long causal rows), so there the absolute
+    tolerance applies alone."""
     D, H, KVH, P, start, n, causal, B = case
     g = rng(1400 + n + start + B)
     L = start + n
@@ -360,12 +368,16 @@ def test_prefill_paired16(gpu, case):
         ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(), pos, 1 / math.sqrt(D),
                             causal, max_query_len=n, path=path)
         outs.append(out)
-    assert torch.equal(outs[0], outs[2])                 # AUTO takes it
+    if (start, n, B) in PAIRED16_AUTO:
+        assert torch.equal(outs[0], outs[2])             # AUTO takes it
     got = outs[0].float().cpu().numpy()
     assert float(np.max(np.abs(got - outs[1].float().cpu().numpy()))) <= 2e-2
     for b in range(B):
         ref = orc.attention(q[b * n:(b + 1) * n], bts[b], start, 1 / math.sqrt(D), causal, kp, vp)
-        check(ref, got[b * n:(b + 1) * n], True)
+        if n <= 512:
+            check(ref, got[b * n:(b + 1) * n], True)
+        else:
+            assert float(np.max(np.abs(ref - got[b * n:(b + 1) * n]))) <= TOL[True]
 
 # (head_dim, heads, kv_heads, page_size, start, n, table width in pages, dtype)
 NARROW_CASES = [(128, 32, 8, 16, 200, 1, 5, "bf16"), (128, 32, 8, 16, 0, 300, 7, "bf16"),

@@ -1117,16 +1117,20 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
                       a->path == TI_PATH_PREFILL_PAIRED16 ||
                       (a->path != TI_PATH_PREFILL_STAGED && pl.wpg == 2));
     // Paired q-tiles (a heavy and a light 32-row q-tile per work-group, equal causal work
-    // per work-group) for the two-wave, four-group direct-load shape of causal steps
-    // without key splits; G must divide 32 (whole positions per 32-row q-tile).
-    pl.pair = pl.dl && a->causal && pl.wpg == 2 && pl.ng == 4 && pl.splits == 1 && 32 % G == 0 &&
-              (a->path == TI_PATH_PREFILL_PAIRED || a->path == TI_PATH_PREFILL_PAIRED16 ||
-               ((a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO) &&
-                                                     PAIR_BY_DEFAULT));
-    // The paired work-groups on 16-row waves (prefill16_kernel) unless the 32-row paired
-    // kernel is pinned: measured 11.4 -> 10.4 us at a 512-token prefill and 22.0 -> 19.7 us
-    // chunked (512 on 1024), same process.
-    pl.r16 = pl.pair && a->path != TI_PATH_PREFILL_PAIRED && (a->path == TI_PATH_PREFILL_PAIRED16 || R16_BY_DEFAULT);
+    // per work-group) for causal steps without key splits on the direct-load shapes; G
+    // must divide 32 (whole positions per 32-row q-tile). On 16-row waves
+    // (prefill16_kernel) while the pairs make at most 512 work-groups: measured against the
+    // plan's four-wave kernel (same process) 11.4 -> 10.4 us at 512 tokens, 22.0 -> 19.7 us
+    // for 512 on a 1024-token prefix, 27.2 -> 24.6 us at 1024 tokens, 46.3 -> 42.9 us for
+    // 1024 on 1024, even at 768 tokens (384 work-groups), but 37.0 -> 43.3 us at 1536 tokens
+    // (768) and twice as slow from 2048 tokens. The 32-row paired kernel (pinned with
+    // TI_PATH_PREFILL_PAIRED) needs the plan's two-wave, four-group shape.
+    const bool pair_ok = dl_ok && a->causal && pl.splits == 1 && 32 % G == 0;
+    const long long pair_wgs = pairs * (((a->max_query_len + 32 / G - 1) / (32 / G) + 1) / 2);
+    const bool auto_path = a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO;
+    pl.r16 = pair_ok && (a->path == TI_PATH_PREFILL_PAIRED16 || (auto_path && R16_BY_DEFAULT && pair_wgs <= 512));
+    pl.pair = pl.r16 || (pair_ok && pl.dl && pl.wpg == 2 && pl.ng == 4 &&
+                         (a->path == TI_PATH_PREFILL_PAIRED || (auto_path && PAIR_BY_DEFAULT)));
     if (pl.pair) {
         pl.TQ = 32 / G;
         pl.qtiles = (a->max_query_len + pl.TQ - 1) / pl.TQ;
