@@ -1126,7 +1126,8 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     // (768) and twice as slow from 2048 tokens. The 32-row paired kernel (pinned with
     // TI_PATH_PREFILL_PAIRED) needs the plan's two-wave, four-group shape.
     const bool pair_ok = dl_ok && a->causal && pl.splits == 1 && 32 % G == 0;
-    const long long pair_wgs = pairs * (((a->max_query_len + 32 / G - 1) / (32 / G) + 1) / 2);
+    // (32 % G == 0 in pair_ok: G <= 32, so 32 / G >= 1)
+    const long long pair_wgs = pair_ok ? pairs * (((a->max_query_len + 32 / G - 1) / (32 / G) + 1) / 2) : 0;
     const bool auto_path = a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO;
     pl.r16 = pair_ok && (a->path == TI_PATH_PREFILL_PAIRED16 || (auto_path && R16_BY_DEFAULT && pair_wgs <= 512));
     pl.pair = pl.r16 || (pair_ok && pl.dl && pl.wpg == 2 && pl.ng == 4 &&
