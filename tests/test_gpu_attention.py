@@ -208,14 +208,14 @@ def _run_batch(g, starts, counts, use_qsl, KVH=8, H=32, D=128, P=16):
     return q, kp, vp, bts, qsl, out.float().cpu().numpy()
 
 
-# Split batches of 2-64 sequences share their work-groups out by length: one long sequence
-# among short ones (most work-groups on one sequence), an empty sequence, 64 sequences
-# (the largest such batch) and 65 (one split count for all), multi-token steps through
-# query_start_loc and through the uniform layout.
+# Split batches of 4-64 sequences with at least 4 splits each share their work-groups out
+# by length: one long sequence among short ones (most work-groups on one sequence), an
+# empty sequence, 64 sequences (the largest such batch) and 65 (one split count for all),
+# multi-token steps through query_start_loc and through the uniform layout.
 FLAT_CASES = {
     "one_long": ([8000, 15, 16, 17], [1, 1, 1, 1], True),
     "empty_and_multi": ([3000, 700, 0, 40], [3, 0, 5, 8], True),
-    "b64": (None, 64, True),     # with 2 KV heads (128 pairs: 2 splits each)
+    "b64": (None, 64, True),     # with 1 KV head (64 pairs: 4 splits each)
     "b65": (None, 65, True),
     "uniform_layout": ([100, 5000, 2000, 64, 900, 1], [2, 2, 2, 2, 2, 2], False),
 }
@@ -229,7 +229,7 @@ def test_split_shares_by_length(gpu, name):
         B = counts
         starts = [int(x) for x in g.integers(0, 3000, size=B)]
         counts = [1] * B
-        q, kp, vp, bts, qsl, got = _run_batch(g, starts, counts, use_qsl, KVH=2, H=8)
+        q, kp, vp, bts, qsl, got = _run_batch(g, starts, counts, use_qsl, KVH=1, H=4)
     else:
         q, kp, vp, bts, qsl, got = _run_batch(g, starts, counts, use_qsl)
     nmax = max(counts)

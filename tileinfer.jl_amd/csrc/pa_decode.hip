@@ -150,14 +150,18 @@ ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c) 
     }
     if (forced > 0) sp = forced;
     if ((forced_waves == 4 || forced_waves == 8) && pl.rows <= 32) nw = forced_waves;
-    // Split batches of 2-64 sequences share their work-groups out by length (flat mode):
-    // the same B x splits work-groups per KV head, cut in proportion to each sequence's
-    // keys (TI_DECODE_FLAT=0 turns it off, tuning only).
+    // Split batches of 4-64 sequences with at least 4 splits each share their work-groups out
+    // by length (flat mode): the same B x splits work-groups per KV head, cut in proportion
+    // to each sequence's keys (TI_DECODE_FLAT=0 turns it off, tuning only). Measured on
+    // lengths drawn from [1024, 8192] against the fixed splits (separate processes, same
+    // box): B = 8 (4 splits) 31.0 -> 27.5 us, B = 4 (8 splits) 21.3 vs 21.3 us, but B = 2
+    // (16 splits) 16.0 -> 16.9 us and B = 16 (2 splits) 60.8 -> 63.0 us, where the shares
+    // balance little and the device-side prefix costs its latency.
     static const int flat_on = [] {
         const char *e = getenv("TI_DECODE_FLAT");
         return e ? atoi(e) : 1;
     }();
-    pl.flat = flat_on && sp > 1 && a->num_seqs >= 2 && a->num_seqs <= 64 ? sp * a->num_seqs : 0;
+    pl.flat = flat_on && sp >= 4 && a->num_seqs >= 4 && a->num_seqs <= 64 ? sp * a->num_seqs : 0;
     pl.splits = sp;
     pl.waves = nw;
     pl.bytes = sp == 1 ? 0 : (size_t)pairs * sp * pl.rows * (c->head_dim + 2) * sizeof(float);
