@@ -773,7 +773,8 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     constexpr int D = 128, NG = 4, NQB = D / 32, NDB = D / 16;
     constexpr int HW = 2, NQ = 2;        // direct loads: waves per 16-key page half, instructions per wave
     constexpr int RPG = 64, MROW = D + 4;
-    constexpr int SMEM = (int)sizeof(DlSmem) * NG, MERGE = NG * RPG * MROW * 4;
+    constexpr int QOFF = (int)sizeof(DlSmem) * NG;   // the pair's 64 query rows (16 KB)
+    constexpr int SMEM = QOFF + RPG * D * 2, MERGE = NG * RPG * MROW * 4;
     __shared__ __attribute__((aligned(16))) char smem_raw[SMEM > MERGE ? SMEM : MERGE];
     float *mslab = reinterpret_cast<float *>(smem_raw);
 
@@ -795,13 +796,17 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     // This lane's row: row rr of its q-tile (B operand of S^T: elements 32 i + 8 kg .. + 8).
     const int rr = 16 * (wl & 1) + r16, tl = rr / p.G, g = rr - tl * p.G, t = t_first_w + tl;
     const bool row_ok = tl < p.TQ && t < nb && !(light && qt_light == qt);
-    u32x4 qreg[NQB];
+    // The pair's 64 query rows (heavy 0-31, light 32-63) go to LDS with one direct load per
+    // lane (row threadIdx / 16, 16-B slot threadIdx % 16 holding chunk slot ^ (row % 16));
+    // each wave reads its operands back once, after the first barrier.
     {
-        const uint16_t *qr = p.q + ((size_t)(tok0 + (row_ok ? t : 0)) * p.Hq + h * p.G + g) * D;
-#pragma unroll
-        for (int i = 0; i < NQB; i++)
-            qreg[i] = row_ok ? *reinterpret_cast<const u32x4 *>(qr + 32 * i + 8 * kg) : (u32x4){0u, 0u, 0u, 0u};
+        const int qrow = threadIdx.x >> 4, qslot = threadIdx.x & 15, rl = qrow & 31;
+        const int tq = ((qrow >> 5) ? qt_light : qt) * p.TQ + rl / p.G, gq = rl - (rl / p.G) * p.G;
+        const bool ok = rl / p.G < p.TQ && tq < nb;
+        const uint16_t *src = p.q + ((size_t)(tok0 + (ok ? tq : 0)) * p.Hq + h * p.G + gq) * D + (qslot ^ (qrow & 15)) * 8;
+        lds_dma16_v<false>(src, (uint32_t)(uintptr_t)(smem_raw + QOFF) + w * 1024);
     }
+    u32x4 qreg[NQB];
     const TilePages spec = tile_pages(p, bt, grp);   // before the positions: tile grp's pages
     const int start = max(p.positions[tok0], 0), len = start + nb;
     const int qpos = p.causal && row_ok ? start + t : len - 1;
@@ -934,6 +939,15 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
         }
     };
     issue(0, 0);
+    wait_direct_loads();
+    __syncthreads();
+    {
+        const int qr = 32 * (wl >> 1) + rr;   // this lane's row in the query block
+        const uint16_t *qb = reinterpret_cast<const uint16_t *>(smem_raw + QOFF) + qr * D;
+#pragma unroll
+        for (int i = 0; i < NQB; i++)
+            qreg[i] = row_ok ? *reinterpret_cast<const u32x4 *>(qb + (((4 * i + kg) ^ (qr & 15)) * 8)) : (u32x4){0u, 0u, 0u, 0u};
+    }
     for (int i = 0; i < steps; i += 2) {
         wait_direct_loads();
         __syncthreads();
