@@ -143,6 +143,37 @@ def test_attention_int8(gpu, case):
         assert rel < 0.02
 
 
+
+# configs[2]'s shapes (and a 64-token-page and a 1024-token case) on an INT8 cache: AUTO
+# takes the 16-row paired kernel, its tiles staged through registers as bf16.
+INT8_PAIRED_CASES = [(128, 32, 8, 16, 0, 512, True), (128, 32, 8, 16, 1024, 512, True),
+                     (128, 16, 8, 64, 0, 512, True), (128, 32, 8, 16, 0, 1024, True)]
+
+
+@pytest.mark.parametrize("case", INT8_PAIRED_CASES, ids=str)
+def test_attention_int8_paired16(gpu, case):
+    """INT8 cache through TI_PATH_PREFILL_PAIRED16 (AUTO's pick here) against the oracle over
+    the dequantized cache, with the reference's INT8 bounds (test/ops/tile.jl:237-259)."""
+    D, H, KVH, P, start, n, causal = case
+    c = make_case(case, True, seed=hash(case) % 10000 + 11)
+    g = c["g"]
+    cs = smoothing(g, D)
+    pages = c["kp"].shape[0]
+    k_src = orc.bf16_round(c["kp"] * orc.bf16_round(cs)[None, None, None, :])
+    kq, vq = ti.int8_kv_pools(D, P, KVH, pages, key_smoothing=torch.from_numpy(cs))
+    kk = dev(k_src.transpose(0, 2, 1, 3).reshape(-1, KVH, D), torch.bfloat16)
+    vv = dev(c["vp"].transpose(0, 2, 1, 3).reshape(-1, KVH, D), torch.bfloat16)
+    ti.store_kv_(BE, kq, vq, kk, vv, torch.arange(1, P * pages + 1, dtype=torch.int32, device="cuda"))
+    lq, ls = kq.layer_q.cpu().numpy(), kq.layer_scale.cpu().numpy()
+    ref8 = exact(c, layer_q=lq, layer_scale=ls, smooth=cs)
+    y16 = run_gpu(c, torch.bfloat16, ti.TI_PATH_PREFILL_PAIRED16, kq, vq)
+    assert np.array_equal(y16, run_gpu(c, torch.bfloat16, ti.TI_PATH_AUTO, kq, vq))
+    assert float(np.max(np.abs(ref8 - y16))) <= 2e-2
+    if n <= 512:
+        assert ulps(ref8, y16) <= 14
+    src = exact(c, kp=k_src, vp=c["vp"])
+    assert math.sqrt(float(np.sum((y16 - src) ** 2)) / float(np.sum(src ** 2))) < 0.02
+
 @pytest.mark.parametrize("path", [ti.TI_PATH_AUTO, ti.TI_PATH_PREFILL])
 def test_batched_ragged(gpu, path):
     """B sequences of different lengths and query counts (one empty) in one call."""

@@ -769,11 +769,18 @@ __device__ __forceinline__ void lds_dma16_v(const void *gptr, uint32_t lds) {
 // A step issues the next tile's loads first (into the other buffer, from inline assembly),
 // then reads this tile's keys, runs the score MFMAs and the softmax, and only then reads
 // the values, so key and value operands never occupy registers together.
+template <bool INT8>
 __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     constexpr int D = 128, NG = 4, NQB = D / 32, NDB = D / 16;
     constexpr int HW = 2, NQ = 2;        // direct loads: waves per 16-key page half, instructions per wave
     constexpr int RPG = 64, MROW = D + 4;
-    constexpr int QOFF = (int)sizeof(DlSmem) * NG;   // the pair's 64 query rows (16 KB)
+    // a key group's tiles (bf16, swizzled rows) and, for an INT8 cache, their scales
+    struct Bufs {
+        uint16_t k[2][KT * 128];
+        uint16_t v[2][KT * 128];
+        float sk[2][INT8 ? KT : 1], sv[2][INT8 ? KT : 1];
+    };
+    constexpr int QOFF = (int)sizeof(Bufs) * NG;   // the pair's 64 query rows (16 KB)
     constexpr int SMEM = QOFF + RPG * D * 2, MERGE = NG * RPG * MROW * 4;
     __shared__ __attribute__((aligned(16))) char smem_raw[SMEM > MERGE ? SMEM : MERGE];
     float *mslab = reinterpret_cast<float *>(smem_raw);
@@ -794,7 +801,7 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     const int t_first_w = qtw * p.TQ;
     const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
     // This lane's row: row rr of its q-tile (B operand of S^T: elements 32 i + 8 kg .. + 8).
-    const int rr = 16 * (wl & 1) + r16, tl = rr / p.G, g = rr - tl * p.G, t = t_first_w + tl;
+    const int rr = 16 * (wl & 1) + r16, tl = rr / p.G, t = t_first_w + tl;
     const bool row_ok = tl < p.TQ && t < nb && !(light && qt_light == qt);
     // The pair's 64 query rows (heavy 0-31, light 32-63) go to LDS with one direct load per
     // lane (row threadIdx / 16, 16-B slot threadIdx % 16 holding chunk slot ^ (row % 16));
@@ -817,7 +824,7 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     const int nkt = (kend + KT - 1) / KT;
     const int steps = (nkt + NG - 1) / NG;
     const int mask_from = p.causal ? start + t_first_w : len - 1;
-    DlSmem &dsm = reinterpret_cast<DlSmem *>(smem_raw)[grp];
+    Bufs &dsm = reinterpret_cast<Bufs *>(smem_raw)[grp];
 
     f32x4 o[NDB];
 #pragma unroll
@@ -870,6 +877,46 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
         }
     };
 
+    // INT8 cache: tiles staged through registers. Lane gl of the group's 256 holds 16 bytes
+    // of key gl / 8 (elements 16 (gl % 8) ..) for K and for V, and lanes 0-63 one scale;
+    // stored as bf16 (exact) into the same swizzled rows as the direct loads. Keys past the
+    // step's end read the last key's row (finite values and scales, masked to p = 0).
+    const int gl = 64 * wl + lane, key_l = gl >> 3, part = gl & 7;
+    const size_t half_q = (size_t)p.num_pages * p.Hk * p.P * D;
+    const size_t half_s = (size_t)p.num_pages * p.Hk * p.P;
+    u32x4 stk = {0u, 0u, 0u, 0u}, stv = {0u, 0u, 0u, 0u};
+    float sts = 0.0f;
+    auto i8_row = [&](int kt, int key, const TilePages &tp) -> long long {
+        const int pos0 = kt * KT, kk = min(key, kend - 1 - pos0);
+        const int pg = kk >> 4 ? tp.pg[1] : tp.pg[0];
+        return ((long long)pg * p.Hk + h) * p.P + ((pos0 + (kk & 16)) & (p.P - 1)) + (kk & 15);
+    };
+    auto i8_load = [&](int kt, const TilePages &tp) {
+        const long long row = i8_row(kt, key_l, tp);
+        stk = *reinterpret_cast<const u32x4 *>(p.lq + row * D + 16 * part);
+        stv = *reinterpret_cast<const u32x4 *>(p.lq + half_q + row * D + 16 * part);
+        if (gl < 2 * KT) {
+            const long long srow = i8_row(kt, gl & (KT - 1), tp);
+            sts = p.ls[(gl < KT ? 0 : half_s) + srow];
+        }
+    };
+    auto i8_store = [&](int buf) {
+#pragma unroll
+        for (int c2 = 0; c2 < 2; c2++) {
+            const int c = 2 * part + c2;
+            uint32_t a0, a1, a2, a3;
+            i8x4_to_bf16(stk[2 * c2], a0, a1);
+            i8x4_to_bf16(stk[2 * c2 + 1], a2, a3);
+            *reinterpret_cast<u32x4 *>(&dsm.k[buf][key_l * D + ((c ^ (key_l & 15)) * 8)]) = (u32x4){a0, a1, a2, a3};
+            i8x4_to_bf16(stv[2 * c2], a0, a1);
+            i8x4_to_bf16(stv[2 * c2 + 1], a2, a3);
+            const int vs = c ^ (4 * (key_l & 3)) ^ (2 * ((key_l >> 2) & 1));
+            *reinterpret_cast<u32x4 *>(&dsm.v[buf][key_l * D + vs * 8]) = (u32x4){a0, a1, a2, a3};
+        }
+        if (gl < KT) dsm.sk[buf][gl] = sts;
+        else if (gl < 2 * KT) dsm.sv[buf][gl - KT] = sts;
+    };
+
     auto compute = [&](int kt, int buf, auto &&issue_loads) {
         issue_loads();
         if (kt >= kt_hi_w) return;   // past this wave's keys (a light wave, or the group's last step)
@@ -887,10 +934,17 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
                 sc[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka[i]), as_bf16x8(qreg[i]), sc[kb], 0, 0, 0);
         }
         const bool need_mask = kt * KT + KT - 1 > mask_from;
+        // INT8: the scales of this lane's 8 score keys, 4 kg + e and 16 + 4 kg + e
+        f32x4 skq[2];
+        if constexpr (INT8) {
+            skq[0] = *reinterpret_cast<const f32x4 *>(&dsm.sk[buf][4 * kg]);
+            skq[1] = *reinterpret_cast<const f32x4 *>(&dsm.sk[buf][16 + 4 * kg]);
+        }
         float x[8], mt = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             float v = sc[e >> 2][e & 3];
+            if constexpr (INT8) v *= skq[e >> 2][e & 3];
             if (need_mask) {
                 const int kpos = kt * KT + 16 * (e >> 2) + 4 * kg + (e & 3);
                 v = (kpos <= qpos && kpos < kend_w) ? v : -INFINITY;
@@ -916,6 +970,16 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
             ps += pe[e];
         }
         l += ps;
+        if constexpr (INT8) {
+            // a value's scale multiplies its probability before the bf16 rounding
+            const f32x4 sva = *reinterpret_cast<const f32x4 *>(&dsm.sv[buf][4 * kg]);
+            const f32x4 svb = *reinterpret_cast<const f32x4 *>(&dsm.sv[buf][16 + 4 * kg]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                pe[e] *= sva[e];
+                pe[4 + e] *= svb[e];
+            }
+        }
         const u32x4 pb = {pack_bf16x2(pe[0], pe[1]), pack_bf16x2(pe[2], pe[3]), pack_bf16x2(pe[4], pe[5]),
                           pack_bf16x2(pe[6], pe[7])};
         const uint16_t *vt = &dsm.v[buf][0];
@@ -938,24 +1002,58 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
             pn = tile_pages(p, bt, min(tile_of(i + 1), nkt - 1));
         }
     };
-    issue(0, 0);
-    wait_direct_loads();
+    if constexpr (!INT8) {
+        issue(0, 0);
+    } else {
+        i8_load(min(tile_of(0), nkt - 1), pn);
+        pn = tile_pages(p, bt, min(tile_of(1), nkt - 1));
+        i8_store(0);
+    }
+    wait_direct_loads();   // the queries' direct loads (and tile 0's)
     __syncthreads();
     {
         const int qr = 32 * (wl >> 1) + rr;   // this lane's row in the query block
         const uint16_t *qb = reinterpret_cast<const uint16_t *>(smem_raw + QOFF) + qr * D;
 #pragma unroll
-        for (int i = 0; i < NQB; i++)
-            qreg[i] = row_ok ? *reinterpret_cast<const u32x4 *>(qb + (((4 * i + kg) ^ (qr & 15)) * 8)) : (u32x4){0u, 0u, 0u, 0u};
+        for (int i = 0; i < NQB; i++) {
+            const u32x4 raw = *reinterpret_cast<const u32x4 *>(qb + (((4 * i + kg) ^ (qr & 15)) * 8));
+            if constexpr (INT8) {
+                // bf16(q * smooth) (attention.jl:90-95)
+                const int d0 = 32 * i + 8 * kg;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    qreg[i][e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * p.smooth[d0 + 2 * e],
+                                             __uint_as_float(raw[e] & 0xffff0000u) * p.smooth[d0 + 2 * e + 1]);
+            } else {
+                qreg[i] = raw;
+            }
+            if (!row_ok) qreg[i] = (u32x4){0u, 0u, 0u, 0u};
+        }
     }
-    for (int i = 0; i < steps; i += 2) {
-        wait_direct_loads();
-        __syncthreads();
-        compute(tile_of(i), 0, [&] { issue(i + 1, 1); });
-        if (i + 1 >= steps) break;
-        wait_direct_loads();
-        __syncthreads();
-        compute(tile_of(i + 1), 1, [&] { issue(i + 2, 0); });
+    if constexpr (!INT8) {
+        for (int i = 0; i < steps; i += 2) {
+            if (i > 0) {
+                wait_direct_loads();
+                __syncthreads();
+            }
+            compute(tile_of(i), 0, [&] { issue(i + 1, 1); });
+            if (i + 1 >= steps) break;
+            wait_direct_loads();
+            __syncthreads();
+            compute(tile_of(i + 1), 1, [&] { issue(i + 2, 0); });
+        }
+    } else {
+        for (int i = 0; i < steps; i++) {
+            if (i > 0) __syncthreads();
+            const bool more = i + 1 < steps;
+            compute(tile_of(i), i & 1, [&] {
+                if (more) {
+                    i8_load(min(tile_of(i + 1), nkt - 1), pn);
+                    pn = tile_pages(p, bt, min(tile_of(i + 2), nkt - 1));
+                }
+            });
+            if (more) i8_store((i + 1) & 1);
+        }
     }
     __syncthreads();   // every wave is done with the tiles before the merge reuses the LDS
 
@@ -1139,12 +1237,15 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     // 1024 on 1024, even at 768 tokens (384 work-groups), but 37.0 -> 43.3 us at 1536 tokens
     // (768) and twice as slow from 2048 tokens. The 32-row paired kernel (pinned with
     // TI_PATH_PREFILL_PAIRED) needs the plan's two-wave, four-group shape.
-    const bool pair_ok = dl_ok && a->causal && pl.splits == 1 && 32 % G == 0;
+    // (INT8 caches pair on the 16-row kernel only, its tiles staged through registers)
+    const bool i8_ok = c->kind == TI_KV_INT8 && a->dtype == TI_BF16 && c->head_dim == 128 &&
+                       c->page_size >= 16 && (c->page_size & (c->page_size - 1)) == 0;
+    const bool pair_ok = (dl_ok || i8_ok) && a->causal && pl.splits == 1 && 32 % G == 0;
     // (32 % G == 0 in pair_ok: G <= 32, so 32 / G >= 1)
     const long long pair_wgs = pair_ok ? pairs * (((a->max_query_len + 32 / G - 1) / (32 / G) + 1) / 2) : 0;
     const bool auto_path = a->path == TI_PATH_PREFILL || a->path == TI_PATH_AUTO;
     pl.r16 = pair_ok && (a->path == TI_PATH_PREFILL_PAIRED16 || (auto_path && R16_BY_DEFAULT && pair_wgs <= 512));
-    pl.pair = pl.r16 || (pair_ok && pl.dl && pl.wpg == 2 && pl.ng == 4 &&
+    pl.pair = pl.r16 || (pair_ok && dl_ok && pl.dl && pl.wpg == 2 && pl.ng == 4 &&
                          (a->path == TI_PATH_PREFILL_PAIRED || (auto_path && PAIR_BY_DEFAULT)));
     if (pl.pair) {
         pl.TQ = 32 / G;
@@ -1187,7 +1288,8 @@ int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti
     const int wpg = pl.wpg, ng = pl.ng;
     dim3 grid(c->kv_heads, pl.pair ? (p.qtiles + 1) / 2 : p.qtiles * pl.splits, a->num_seqs);
     if (pl.r16) {
-        prefill16_kernel<<<grid, 1024, 0, s>>>(p);
+        if (c->kind == TI_KV_INT8) prefill16_kernel<true><<<grid, 1024, 0, s>>>(p);
+        else prefill16_kernel<false><<<grid, 1024, 0, s>>>(p);
         return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
     }
     const bool int8 = c->kind == TI_KV_INT8;
