@@ -723,7 +723,10 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
 // per-lane 32-bit byte offset; NT: cache-policy bits sc0 nt). The compiler does not see
 // its LDS write, so it adds no waits of its own before LDS reads of the other buffer; the
 // caller waits with an explicit vmcnt and a barrier before any wave reads the tile.
-// lds_addr is wave-uniform (it goes to M0).
+// lds_addr is wave-uniform (it goes to M0). M0 cannot be declared clobbered (the compiler
+// reserves it); the kernel that uses these helpers has no other use of M0 (gfx9 LDS
+// instructions need no M0 set-up, and it indexes no register arrays dynamically; its gfx950
+// assembly has no M0 write besides these statements).
 template <bool NT>
 __device__ __forceinline__ void lds_dma16(const void *base, uint32_t voff, uint32_t lds) {
     // the base and the LDS address are wave-uniform: pin them in scalar registers
