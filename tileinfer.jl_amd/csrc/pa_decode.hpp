@@ -223,10 +223,14 @@ __device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodePara
                 t.v[e] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(vb + (vr[e] * D + vc * 8)));
         } else {
             const int8_t *kb = p.lq + r0 * D, *vb = p.lq + half_q + r0 * D;
+            // keys in 16-B pieces (64 contiguous bytes per row across a lane group, against
+            // 32 with 8-B pieces: 1 % faster); score MFMA 2 u + c takes bytes 64 u + 16 kg +
+            // 8 c, and the queries' head dimension is gathered in the same order
 #pragma unroll
-            for (int i = 0; i < NKB; i++) {
-                const uint2 r = *reinterpret_cast<const uint2 *>(kb + (kr * D + i * 32 + kg * 8));
-                t.k[i] = (u32x4){r.x, r.y, 0u, 0u};
+            for (int u = 0; u < NKB / 2; u++) {
+                const u32x4 r = *reinterpret_cast<const u32x4 *>(kb + (kr * D + u * 64 + kg * 16));
+                t.k[2 * u] = (u32x4){r[0], r[1], 0u, 0u};
+                t.k[2 * u + 1] = (u32x4){r[2], r[3], 0u, 0u};
             }
 #pragma unroll
             for (int e = 0; e < KPL; e++) {
@@ -252,9 +256,10 @@ __device__ __forceinline__ void load_tile(TileRegs<D, INT8> &t, const DecodePara
             t.v[e] = *reinterpret_cast<const u32x4 *>(p.vp + vrow[e] * D + vc * 8);
     } else {
 #pragma unroll
-        for (int i = 0; i < NKB; i++) {
-            const uint2 r = *reinterpret_cast<const uint2 *>(p.lq + krow * D + i * 32 + kg * 8);
-            t.k[i] = (u32x4){r.x, r.y, 0u, 0u};
+        for (int u = 0; u < NKB / 2; u++) {
+            const u32x4 r = *reinterpret_cast<const u32x4 *>(p.lq + krow * D + u * 64 + kg * 16);
+            t.k[2 * u] = (u32x4){r[0], r[1], 0u, 0u};
+            t.k[2 * u + 1] = (u32x4){r[2], r[3], 0u, 0u};
         }
 #pragma unroll
         for (int e = 0; e < KPL; e++) {
@@ -346,7 +351,7 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
             float qf[NKB][8], amax = 0.0f;
 #pragma unroll
             for (int i = 0; i < NKB; i++) {
-                const int d0 = i * 32 + kg * 8;
+                const int d0 = (i >> 1) * 64 + kg * 16 + (i & 1) * 8;   // the keys' 16-B loads' order
                 const u32x4 raw = ok ? *reinterpret_cast<const u32x4 *>(qr + d0) : (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
