@@ -502,11 +502,13 @@ __global__ void __launch_bounds__(NW * 64) decode_kernel(DecodeParams p) {
     };
 
     // Two register sets, ping-ponged: the next group of TPI tiles is loading while the
-    // current one computes. INT8 tiles are half the bytes, so INT8 waves take two tiles
-    // per step to keep as many bytes in flight as bf16 waves. The prefetch is issued
+    // current one computes. INT8 tiles are half the bytes, so INT8 waves take more tiles
+    // per step: three for 16-row waves (configs[3], Llama-3-8B B = 8 x 32768, same process:
+    // 96.5-98.6 us with two, 94.2-94.7 with three, 100-102 with four, 104-106 with one),
+    // two for 32-row waves, whose accumulators leave less room. The prefetch is issued
     // unconditionally (past the last tile it re-reads that tile, unused) so the count of
     // loads in flight is static and each wait covers only the tiles in use.
-    constexpr int TPI = INT8 ? 2 : 1;
+    constexpr int TPI = INT8 ? (ROWB == 1 ? 3 : 2) : 1;
     constexpr int STRIDE = NKW * TPI;
     TileRegs<D, INT8> ta[TPI], tb[TPI];
     auto ld = [&](TileRegs<D, INT8> (&t)[TPI], int jj) {
