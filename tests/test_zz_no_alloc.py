@@ -28,6 +28,10 @@ CASES = [
     ("prefill_4w_splits", "bf16", 32, 8, 16, [(1, 1024, 64), (1, 300, 40)], _lib.TI_PATH_PREFILL_DIRECT),
     ("decode_int8", "int8", 32, 8, 16, [(2, 3000, 1), (2, 700, 1)], _lib.TI_PATH_AUTO),
     ("generic_fp32", "fp32", 16, 8, 16, [(1, 1023, 1), (1, 200, 1)], _lib.TI_PATH_AUTO),
+    # split batches shared out by length (flat mode) and the 16-row paired prefill (bf16, INT8)
+    ("decode_flat", "bf16", 32, 8, 16, [(6, 3000, 1), (4, 700, 1)], _lib.TI_PATH_AUTO),
+    ("prefill_paired16", "bf16", 32, 8, 16, [(1, 0, 512), (1, 1024, 128)], _lib.TI_PATH_AUTO),
+    ("prefill_paired16_int8", "int8", 32, 8, 16, [(1, 0, 512), (1, 300, 200)], _lib.TI_PATH_AUTO),
 ]
 
 
