@@ -55,10 +55,12 @@ def test_decode_step_graph_replays_as_sequences_grow(gpu, B, n):
         assert torch.equal(got, ref), f"replay {step} differs from eager"
 
 
-@pytest.mark.parametrize("path", [ti.TI_PATH_AUTO, ti.TI_PATH_PREFILL_PINGPONG])
-def test_prefill_and_kv_write_graph(gpu, path):
-    """AUTO's choice, and the 8-wave ping-pong prefill kernel pinned."""
-    Hq, Hk, D, P, n = 32, 8, 128, 16, 128
+@pytest.mark.parametrize("path,n", [(ti.TI_PATH_AUTO, 128), (ti.TI_PATH_PREFILL_PINGPONG, 128),
+                                    (ti.TI_PATH_AUTO, 512)])
+def test_prefill_and_kv_write_graph(gpu, path, n):
+    """AUTO's choice (128 new tokens: the four-wave kernel with key splits; 512: the 16-row
+    paired kernel), and the 8-wave ping-pong prefill kernel pinned."""
+    Hq, Hk, D, P = 32, 8, 128, 16
     torch.manual_seed(7)
     pages = 64
     k = torch.randn((pages, Hk, P, D), device="cuda", dtype=torch.bfloat16)
