@@ -753,8 +753,9 @@ __device__ __forceinline__ void lds_dma16_v(const void *gptr, uint32_t lds) {
         asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory");
 }
 
-// Paired q-tiles on 16-row waves (bf16 dense cache, D = 128, pages of 2^k >= 16 tokens,
-// causal, no key splits). The work of the paired kernel above — work-group y holds the
+// Paired q-tiles on 16-row waves (bf16 activations, D = 128, pages of 2^k >= 16 tokens,
+// causal, no key splits; dense bf16 cache, or INT8 with INT8 = true). The work of the paired
+// kernel above — work-group y holds the
 // heavy q-tile qtiles - 1 - y and the light q-tile y, four key groups walk the key tiles
 // through their own double-buffered LDS tiles and merge at the end — with each q-tile's 32
 // rows split over two waves of 16 rows: 16 waves of at most 128 VGPRs, four per SIMD.
@@ -769,9 +770,12 @@ __device__ __forceinline__ void lds_dma16_v(const void *gptr, uint32_t lds) {
 //   O^T += V^T P^T  D/16 v_mfma_f32_16x16x32_bf16; B = P^T is the score registers (k-index
 //                   8 kg + j: key 4 kg + j, then 16 + 4 kg + j - 4), A = V^T from two 8-B
 //                   transposing reads (rows 4 kg .. + 3 and 16 + 4 kg .. + 3).
-// A step issues the next tile's loads first (into the other buffer, from inline assembly),
-// then reads this tile's keys, runs the score MFMAs and the softmax, and only then reads
-// the values, so key and value operands never occupy registers together.
+// A step issues the next tile's loads first (dense: direct loads into the other buffer,
+// from inline assembly; INT8: loads into registers, converted to bf16 and stored into the
+// other buffer after the step's compute), then reads this tile's keys, runs the score MFMAs
+// and the softmax, and only then reads the values, so key and value operands never occupy
+// registers together. The pair's 64 query rows come through LDS (one direct load per lane),
+// read once into registers after the first tile lands.
 template <bool INT8>
 __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     constexpr int D = 128, NG = 4, NQB = D / 32, NDB = D / 16;
