@@ -75,11 +75,14 @@ def test_workspace_bytes_decode_and_prefill():
     assert ws(_args(num_seqs=32, total_tokens=32), _cache()) == (0, 0)
     st, n = ws(_args(max_query_len=512, total_tokens=2048), _cache())
     assert st == 0 and n == 0                   # prefill needs none
-    # fp32 (VALU kernel): 4 seqs x 32 heads = 128 waves -> 8 key splits, 4 packed rows each
+    # fp32 (matrix-core decode): 4 seqs x 8 KV heads = 32 pairs -> 16 key splits (512
+    # work-groups), 4 packed rows each
     st, n = ws(_args(dtype=0), _cache())
-    assert st == 0 and n == 4 * 8 * 8 * 4 * 130 * 4
-    # fp32 with 1024 query waves needs no splits
-    assert ws(_args(dtype=0, num_seqs=32, total_tokens=32), _cache()) == (0, 0)
+    assert st == 0 and n == 4 * 8 * 16 * 4 * 130 * 4
+    # 32 seqs: 256 pairs -> 2 splits
+    assert ws(_args(dtype=0, num_seqs=32, total_tokens=32), _cache()) == (0, 32 * 8 * 2 * 4 * 130 * 4)
+    # fp32 with 8-token pages runs the VALU kernel: 1024 query waves need no splits
+    assert ws(_args(dtype=0, num_seqs=32, total_tokens=32), _cache(page_size=8)) == (0, 0)
     # independent of context length / pool size: same for a larger pool
     assert ws(_args(), _cache(num_pages=100000))[1] == ws(_args(), _cache())[1]
 

@@ -211,7 +211,7 @@ def test_batched_ragged(gpu, path):
         check(ref, got[qsl[b]:qsl[b + 1]], True)
 
 
-def _run_batch(g, starts, counts, use_qsl, KVH=8, H=32, D=128, P=16):
+def _run_batch(g, starts, counts, use_qsl, KVH=8, H=32, D=128, P=16, bf16=True, causal=True):
     """One call over sequences at `starts` with `counts` query tokens each; returns
     (q, kp, vp, bts, qsl, out). Without `use_qsl` every sequence has max(counts) tokens."""
     nmax = max(counts)
@@ -224,16 +224,17 @@ def _run_batch(g, starts, counts, use_qsl, KVH=8, H=32, D=128, P=16):
         used = -(-(s + n) // P)
         bts[b, :used] = perm[off:off + used]
         off += used
-    kp, vp = randn(g, pages, KVH, P, D, bf16=True), randn(g, pages, KVH, P, D, bf16=True)
-    q = randn(g, sum(counts), H, D, bf16=True)
+    kp, vp = randn(g, pages, KVH, P, D, bf16=bf16), randn(g, pages, KVH, P, D, bf16=bf16)
+    q = randn(g, sum(counts), H, D, bf16=bf16)
     qsl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     positions = np.concatenate([np.arange(s, s + n) for s, n in zip(starts, counts)]).astype(np.int32)
-    qd = dev(q, torch.bfloat16)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    qd = dev(q, dt)
     out = torch.zeros_like(qd)
-    kd, vd = dev(kp, torch.bfloat16), dev(vp, torch.bfloat16)
+    kd, vd = dev(kp, dt), dev(vp, dt)
     ws = ti.attention_workspace(BE, qd, kd, num_seqs=len(starts), max_query_len=nmax)
     ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(),
-                        torch.from_numpy(positions).cuda(), 1 / math.sqrt(D), True,
+                        torch.from_numpy(positions).cuda(), 1 / math.sqrt(D), causal,
                         query_start_loc=torch.from_numpy(qsl).cuda() if use_qsl else None,
                         max_query_len=nmax)
     return q, kp, vp, bts, qsl, out.float().cpu().numpy()
@@ -270,6 +271,35 @@ def test_split_shares_by_length(gpu, name):
         lo = qsl[b] if use_qsl else b * nmax
         ref = orc.attention(q[lo:lo + n], bts[b], s, 1 / math.sqrt(128), True, kp, vp)
         check(ref, got[lo:lo + n], True)
+
+
+# fp32 batches on the matrix-core decode kernel (dense pools, 2^k >= 16-token pages, at most
+# 16 packed rows): contexts either side of the 16-key tile and of the 4-tile minimum split
+# (one split alone writes the output; longer ones merge only the splits that held keys), 16
+# packed rows (G = 2 x 8 tokens), G = 8 x 2 tokens in the uniform layout, head_dim 64 on
+# 64-token pages, and a non-causal multi-token step.
+# name: (starts, counts, use_qsl, dict(KVH, H, D, P, causal))
+F32_BATCHES = {
+    "split_edges": ([0, 14, 15, 63, 64, 1000, 4100], [1] * 7, True, dict(KVH=8, H=16)),
+    "rows16": ([30, 2000, 500], [8, 8, 3], True, dict(KVH=8, H=16)),
+    "g8_uniform": ([3000, 17], [2, 2], False, dict(KVH=4, H=32)),
+    "d64_p64": ([5000, 60, 191], [1, 1, 1], True, dict(KVH=2, H=8, D=64, P=64)),
+    "non_causal": ([700, 33], [4, 4], True, dict(KVH=8, H=32, causal=False)),
+}
+
+
+@pytest.mark.parametrize("name", list(F32_BATCHES))
+def test_fp32_decode_batches(gpu, name):
+    g = rng(990 + list(F32_BATCHES).index(name))
+    starts, counts, use_qsl, kw = F32_BATCHES[name]
+    causal = kw.get("causal", True)
+    q, kp, vp, bts, qsl, got = _run_batch(g, starts, counts, use_qsl, bf16=False, **kw)
+    nmax = max(counts)
+    D = kw.get("D", 128)
+    for b, (s, n) in enumerate(zip(starts, counts)):
+        lo = qsl[b] if use_qsl else b * nmax
+        ref = orc.attention(q[lo:lo + n], bts[b], s, 1 / math.sqrt(D), causal, kp, vp)
+        check(ref, got[lo:lo + n], False)
 
 
 # (head_dim, heads, kv_heads, page_size, start, n, causal, block-table width in pages)

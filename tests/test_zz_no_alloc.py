@@ -27,7 +27,10 @@ CASES = [
     ("prefill_pp_splits", "bf16", 8, 1, 16, [(1, 0, 256), (1, 0, 100)], _lib.TI_PATH_PREFILL_PINGPONG),
     ("prefill_4w_splits", "bf16", 32, 8, 16, [(1, 1024, 64), (1, 300, 40)], _lib.TI_PATH_PREFILL_DIRECT),
     ("decode_int8", "int8", 32, 8, 16, [(2, 3000, 1), (2, 700, 1)], _lib.TI_PATH_AUTO),
-    ("generic_fp32", "fp32", 16, 8, 16, [(1, 1023, 1), (1, 200, 1)], _lib.TI_PATH_AUTO),
+    # fp32 on the matrix-core decode kernel (16-token pages; the second call has fewer active
+    # splits), and on the VALU kernel (8-token pages)
+    ("fp32_mfma", "fp32", 16, 8, 16, [(1, 4095, 1), (1, 200, 1)], _lib.TI_PATH_AUTO),
+    ("generic_fp32", "fp32", 16, 8, 8, [(1, 1023, 1), (1, 200, 1)], _lib.TI_PATH_AUTO),
     # split batches shared out by length (flat mode) and the 16-row paired prefill (bf16, INT8)
     ("decode_flat", "bf16", 32, 8, 16, [(6, 3000, 1), (4, 700, 1)], _lib.TI_PATH_AUTO),
     ("prefill_paired16", "bf16", 32, 8, 16, [(1, 0, 512), (1, 1024, 128)], _lib.TI_PATH_AUTO),

@@ -87,6 +87,17 @@ __device__ __forceinline__ int page_of(const int32_t *bt, int idx, int bt_stride
 // The same lookup for a wave-uniform index, as a scalar load through the constant address
 // space: it is counted by lgkmcnt, so waiting for it never waits for the vector loads of
 // prefetched tiles (vmcnt is in order).
+// Key splits that hold keys when every split takes at least `min_tiles` 16-key tiles (the
+// fp32 matrix-core decode): the first `active` of the launch's `splits` work-groups take
+// `per` tiles each, the rest have none and write nothing.
+struct ActiveSplits {
+    int per, active;
+};
+__device__ __forceinline__ ActiveSplits f32_active_splits(int ntiles, int splits, int min_tiles) {
+    const int per = max((ntiles + splits - 1) / splits, min_tiles);
+    return {per, (ntiles + per - 1) / per};
+}
+
 __device__ __forceinline__ int page_of_s(const int32_t *bt, int idx, int bt_stride, int num_pages) {
     idx = __builtin_amdgcn_readfirstlane(idx);
     idx = idx < 0 ? 0 : (idx >= bt_stride ? bt_stride - 1 : idx);
@@ -125,9 +136,10 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
                      hipStream_t s);
 // Merge split partials [B][Hk][splits][rows][D + 2] from a->workspace into a->out; flat
 // mode (flat work-groups per KV head): partials [Hk][flat][rows][D + 2], each sequence's
-// pieces located by the decode kernel's table at meta.
+// pieces located by the decode kernel's table at meta. min_tiles > 0: a sequence's splits
+// took at least min_tiles 16-key tiles each, and only those that held keys are merged.
 int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows, int splits,
-                      hipStream_t s, int flat = 0, int *meta = nullptr);
+                      hipStream_t s, int flat = 0, int *meta = nullptr, int min_tiles = 0);
 
 struct ti_prefill_plan {
     int pp;          // 1: the 8-wave ping-pong kernel (pa_prefill_pp.hip)

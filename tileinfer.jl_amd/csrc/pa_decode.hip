@@ -31,6 +31,11 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
         if (mt.y <= 1) return;
         splits = mt.y;
         first = (size_t)h * p.flat + mt.x;
+    } else if (p.min_tiles > 0) {
+        // only the splits that held keys wrote partials
+        const int len = max(p.positions[tok0], 0) + nb;
+        splits = f32_active_splits((len + 15) >> 4, p.splits, p.min_tiles).active;
+        if (splits <= 1) return;   // the one split wrote the output itself
     }
     const float *base = p.part + first * stride + (size_t)r * (D + 2);
     // Splits in batches of SB (2, 4, 8 or 16: the launch takes the smallest that holds all
@@ -216,8 +221,10 @@ int ti_launch_decode(const ti_attention_args *a, const ti_kv_cache *c, const ti_
 }
 
 int ti_launch_combine(const ti_attention_args *a, const ti_kv_cache *c, int rows, int splits,
-                      hipStream_t s, int flat, int *meta) {
+                      hipStream_t s, int flat, int *meta, int min_tiles) {
     DecodeParams p{};
+    p.min_tiles = min_tiles;
+    p.positions = a->positions;
     p.out = (uint16_t *)a->out;
     p.part = (float *)a->workspace;
     p.flat = flat;

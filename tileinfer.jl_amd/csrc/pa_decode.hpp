@@ -60,6 +60,7 @@ struct DecodeParams {
     int *meta;   // flat mode: per sequence {first work-group, pieces}, written by the decode kernel
     int bt_stride, num_pages, P, pshift, Hk, Hq, G, nmax, M, splits, causal;
     int B, flat;   // flat: work-groups per KV head shared by all sequences (0: `splits` each)
+    int min_tiles;   // > 0: splits of at least this many 16-key tiles (f32_active_splits)
     float scale_log2;
 };
 

@@ -128,6 +128,161 @@ __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) 
     }
 }
 
+// Float32 decode on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 products and
+// sums, within the fp32 path's 1e-4 tolerance), for dense fp32 pools with 16-key tiles in one
+// page (P a power of two >= 16), D = 64 or 128 and at most 16 packed query rows (g + G t, as
+// the bf16 decode kernel). Work-group = (key split, KV head, sequence), four waves taking every
+// fourth 16-key tile of the split. Per tile and wave (lane l: row r16 = l % 16, k-group kg =
+// l / 16):
+//   S^T = K Q^T     D/4 MFMAs; MFMA (j, c) sums head-dim elements 16 j + 4 kg' + c over kg'
+//                   (lane: key r16's and row r16's element 16 j + 4 kg + c, from float4 loads);
+//                   the lane gets its row's scores of keys 4 kg + e.
+//   softmax         exp2 domain, lane-local per row (two xor shuffles for a row max; lazy
+//                   rescale as the bf16 kernel).
+//   O^T += V^T P^T  4 D/16 MFMAs; MFMA (e, db): A = V[key 4 kg + e][16 db + r16] (a
+//                   coalesced row read), B = the lane's probability of key 4 kg + e.
+// The waves merge through LDS; one split writes the output, more write Float32 partials in
+// the decode kernel's layout for the combine kernel.
+struct F32DecodeParams {
+    const float *q;
+    float *out;
+    const float *kp, *vp;
+    const int32_t *positions, *qsl, *bt;
+    float *part;
+    int bt_stride, num_pages, P, pshift, Hk, Hq, G, nmax, M, splits, causal;
+    float scale_log2;
+};
+
+// Each split takes at least this many 16-key tiles (one per wave), so short contexts run on
+// fewer work-groups than the launch holds.
+constexpr int F32_MIN_TILES = 4;
+
+template <int D>
+__global__ void __launch_bounds__(256) decode_f32_kernel(F32DecodeParams p) {
+    constexpr int NJ = D / 16, NDB = D / 16, NW = 4, MROW = D + 4;
+    __shared__ __attribute__((aligned(16))) float slab[NW * 16 * MROW];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r16 = lane & 15, kg = lane >> 4;
+    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
+    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
+    if (nb <= 0) return;
+    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
+    const ActiveSplits as = f32_active_splits((len + 15) >> 4, p.splits, F32_MIN_TILES);
+    if (s >= as.active) return;   // no keys for this split
+    const int j0 = s * as.per, j1 = min(j0 + as.per, (len + 15) >> 4);
+    const int t = r16 / p.G, g = r16 - t * p.G;
+    const bool ok = r16 < p.M && t < nb;
+    const int qpos = p.causal && ok ? start + t : len - 1;
+    const int mask_from = p.causal ? start : len - 1;   // keys up to here are visible to every row
+    f32x4 qv[NJ];
+    {
+        const float *qr = p.q + ((size_t)(tok0 + (ok ? t : 0)) * p.Hq + h * p.G + g) * D + 4 * kg;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            qv[j] = ok ? *reinterpret_cast<const f32x4 *>(qr + 16 * j) : (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    f32x4 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; db++) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m = NEG_BIG, l = 0.0f;
+    const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
+    for (int j = j0 + w; j < j1; j += NW) {
+        const int pos0 = j * 16, last = len - 1 - pos0;   // keys past len read the last key's row
+        const int pg = page_of_s(bt, pos0 >> p.pshift, p.bt_stride, p.num_pages);
+        const long long rbase = ((long long)pg * p.Hk + h) * p.P + (pos0 & (p.P - 1));
+        const float *krow = p.kp + (rbase + min(r16, last)) * D + 4 * kg;
+        f32x4 kv[NJ];
+#pragma unroll
+        for (int jj = 0; jj < NJ; jj++) kv[jj] = *reinterpret_cast<const f32x4 *>(krow + 16 * jj);
+        float vv[4][NDB];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float *vrow = p.vp + (rbase + min(4 * kg + e, last)) * D + r16;
+#pragma unroll
+            for (int db = 0; db < NDB; db++) vv[e][db] = vrow[16 * db];
+        }
+        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < NJ; jj++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[jj][c], qv[jj][c], sc, 0, 0, 0);
+        const bool need_mask = pos0 + 15 > mask_from;
+        float x[4], mt = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int kpos = pos0 + 4 * kg + e;
+            x[e] = need_mask && kpos > qpos ? -INFINITY : sc[e];
+            mt = fmaxf(mt, x[e]);
+        }
+        mt *= p.scale_log2;
+        if (__any(mt > m + 8.0f)) {
+            mt = fmaxf(mt, __shfl_xor(mt, 16));
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float mn = fmaxf(m, mt);
+            const float alpha = fast_exp2(m - mn);
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; db++) o[db] *= alpha;
+        }
+        float pe[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            pe[e] = fast_exp2(__builtin_fmaf(x[e], p.scale_log2, -m));
+            l += pe[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int db = 0; db < NDB; db++) o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[e][db], pe[e], o[db], 0, 0, 0);
+    }
+    // merge the four waves' states (same rows, disjoint keys) through LDS
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    {
+        float *my = slab + ((size_t)w * 16 + r16) * MROW;
+#pragma unroll
+        for (int db = 0; db < NDB; db++) *reinterpret_cast<f32x4 *>(my + 16 * db + 4 * kg) = o[db];
+        if (kg == 0) {
+            my[D] = m;
+            my[D + 1] = l;
+        }
+    }
+    __syncthreads();
+    const size_t unit = ((size_t)b * p.Hk + h) * p.splits + s;
+    for (int item = threadIdx.x; item < p.M * (D / 4); item += NW * 64) {
+        const int r = item / (D / 4), d4 = (item % (D / 4)) * 4;
+        float mx = NEG_BIG;
+#pragma unroll
+        for (int wi = 0; wi < NW; wi++) mx = fmaxf(mx, slab[((size_t)wi * 16 + r) * MROW + D]);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        float lsum = 0.0f;
+#pragma unroll
+        for (int wi = 0; wi < NW; wi++) {
+            const float *src = slab + ((size_t)wi * 16 + r) * MROW;
+            const float wgt = fast_exp2(src[D] - mx);
+            lsum += src[D + 1] * wgt;
+            acc += *reinterpret_cast<const f32x4 *>(src + d4) * wgt;
+        }
+        const int tr = r / p.G, gr = r - tr * p.G;
+        if (tr >= nb) continue;
+        if (as.active == 1) {
+            const float inv = 1.0f / lsum;
+            *reinterpret_cast<f32x4 *>(p.out + ((size_t)(tok0 + tr) * p.Hq + h * p.G + gr) * D + d4) = acc * inv;
+        } else {
+            float *dst = p.part + (unit * (size_t)p.M + r) * (D + 2);
+#pragma unroll
+            for (int e = 0; e < 4; e++) dst[d4 + e] = acc[e];
+            if (d4 == 0) {
+                dst[D] = mx;
+                dst[D + 1] = lsum;
+            }
+        }
+    }
+}
+
 template <typename T, bool INT8>
 void launch(const GenericParams &p, int D, dim3 grid, hipStream_t s) {
     if (D == 128) generic_attention_kernel<T, INT8, 128><<<grid, 64, 0, s>>>(p);
@@ -136,9 +291,32 @@ void launch(const GenericParams &p, int D, dim3 grid, hipStream_t s) {
 
 }  // namespace
 
+// fp32 steps that the matrix-core decode kernel takes: dense fp32 pools, pages of 2^k >= 16
+// tokens, D = 64 or 128, at most 16 packed query rows. Its key splits: while the (sequence,
+// KV head) pairs times splits are fewer than F32_TARGET work-groups, double (at most 32);
+// short contexts then use fewer of them (F32_MIN_TILES).
+constexpr int F32_TARGET = 512, F32_MAX_SPLITS = 32;
+static bool f32_mfma(const ti_attention_args *a, const ti_kv_cache *c) {
+    const int G = a->q_heads / c->kv_heads;
+    return a->dtype == TI_F32 && c->kind == TI_KV_DENSE && (c->head_dim == 64 || c->head_dim == 128) &&
+           c->page_size >= 16 && (c->page_size & (c->page_size - 1)) == 0 && G * a->max_query_len <= 16;
+}
+static int f32_splits(const ti_attention_args *a, const ti_kv_cache *c) {
+    const long long pairs = (long long)a->num_seqs * c->kv_heads;
+    int sp = 1;
+    while (sp < F32_MAX_SPLITS && pairs * sp < F32_TARGET) sp <<= 1;
+    return sp;
+}
+
 // Key splits for the fp32 path: while the waves (tokens x query heads x sequences) are
 // fewer than about 1024, double the splits (at most 32). Host shapes only (graph-safe).
 int ti_plan_generic(const ti_attention_args *a, const ti_kv_cache *c, size_t *bytes) {
+    if (f32_mfma(a, c)) {
+        const int sp = f32_splits(a, c);
+        const int rows = a->q_heads / c->kv_heads * a->max_query_len;
+        *bytes = sp == 1 ? 0 : (size_t)a->num_seqs * c->kv_heads * sp * rows * (c->head_dim + 2) * sizeof(float);
+        return sp;
+    }
     const long long waves = (long long)a->max_query_len * a->q_heads * a->num_seqs;
     int sp = 1;
     while (sp < 32 && waves * sp < 1024) sp <<= 1;
@@ -148,6 +326,36 @@ int ti_plan_generic(const ti_attention_args *a, const ti_kv_cache *c, size_t *by
 }
 
 int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s) {
+    if (f32_mfma(a, c)) {
+        F32DecodeParams f;
+        f.q = (const float *)a->q;
+        f.out = (float *)a->out;
+        f.kp = (const float *)c->k_pages;
+        f.vp = (const float *)c->v_pages;
+        f.positions = a->positions;
+        f.qsl = a->query_start_loc;
+        f.bt = a->block_tables;
+        f.bt_stride = a->block_table_stride;
+        f.num_pages = c->num_pages;
+        f.P = c->page_size;
+        f.pshift = __builtin_ctz(c->page_size);
+        f.Hk = c->kv_heads;
+        f.Hq = a->q_heads;
+        f.G = a->q_heads / c->kv_heads;
+        f.nmax = a->max_query_len;
+        f.M = f.G * a->max_query_len;
+        f.causal = a->causal;
+        f.scale_log2 = a->scale * LOG2E;
+        size_t bytes = 0;
+        f.splits = ti_plan_generic(a, c, &bytes);
+        if (bytes > 0 && (!a->workspace || a->workspace_bytes < bytes)) f.splits = 1;   // runs unsplit
+        f.part = (float *)a->workspace;
+        const dim3 grid(f.splits, c->kv_heads, a->num_seqs);
+        if (c->head_dim == 128) decode_f32_kernel<128><<<grid, 256, 0, s>>>(f);
+        else decode_f32_kernel<64><<<grid, 256, 0, s>>>(f);
+        if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
+        return f.splits > 1 ? ti_launch_combine(a, c, f.M, f.splits, s, 0, nullptr, F32_MIN_TILES) : TI_OK;
+    }
     GenericParams p;
     p.q = a->q;
     p.out = a->out;
