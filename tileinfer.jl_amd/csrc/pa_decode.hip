@@ -16,28 +16,35 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int h = blockIdx.y, b = blockIdx.z;
-    if (r >= p.M) return;
-    const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
+    // The partial loads wait only for what fixes their addresses: nothing beyond the
+    // arguments, or the flat table's entry, loaded together with the sequence's token range
+    // (query_start_loc); the row and token checks come before the store.
+    const int rr = min(r, p.M - 1);
+    int tok0 = b * p.nmax, tok1 = tok0 + p.nmax;
+    int2 mt = make_int2(0, p.splits);
+    if (p.qsl && p.flat) {
+        tok0 = p.qsl[b];
+        tok1 = p.qsl[b + 1];
+        mt = *reinterpret_cast<const int2 *>(p.meta + 2 * b);
+    } else if (p.qsl) {
+        tok0 = p.qsl[b];
+        tok1 = p.qsl[b + 1];
+    } else if (p.flat) {
+        mt = *reinterpret_cast<const int2 *>(p.meta + 2 * b);
+    }
     const int t = r / p.G, g = r - t * p.G;
-    if (t >= nb) return;
     const size_t stride = (size_t)p.M * (D + 2);
     // flat mode: the sequence's pieces are partial slots lo .. lo + n - 1 of the KV head; a
-    // sequence of one piece had its output written by the decode kernel
-    int splits = p.splits;
-    size_t first = ((size_t)b * p.Hk + h) * p.splits;
-    if (p.flat) {
-        const int2 mt = *reinterpret_cast<const int2 *>(p.meta + 2 * b);
-        if (mt.y <= 1) return;
-        splits = mt.y;
-        first = (size_t)h * p.flat + mt.x;
-    } else if (p.min_tiles > 0) {
-        // only the splits that held keys wrote partials
-        const int len = max(p.positions[tok0], 0) + nb;
+    // sequence of one piece (or none) had its output written by the decode kernel
+    int splits = p.flat ? mt.y : p.splits;
+    const size_t first = p.flat ? (size_t)h * p.flat + mt.x : ((size_t)b * p.Hk + h) * p.splits;
+    if (!p.flat && p.min_tiles > 0) {
+        // only the splits that held keys wrote partials; one alone wrote the output itself
+        const int len = max(p.positions[tok0], 0) + min(tok1 - tok0, p.nmax);
         splits = f32_active_splits((len + 15) >> 4, p.splits, p.min_tiles).active;
-        if (splits <= 1) return;   // the one split wrote the output itself
     }
-    const float *base = p.part + first * stride + (size_t)r * (D + 2);
+    const int last = max(splits, 1) - 1;   // loads stay inside the sequence's slots
+    const float *base = p.part + first * stride + (size_t)rr * (D + 2);
     // Splits in batches of SB (2, 4, 8 or 16: the launch takes the smallest that holds all
     // splits): every load of a batch (m, l and the row) is issued before any arithmetic,
     // and batches merge online, so up to SB splits cost one round trip.
@@ -49,7 +56,7 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
         float dv[SB][PER];
 #pragma unroll
         for (int j = 0; j < SB; j++) {
-            const float *src = base + min(sp0 + j, splits - 1) * stride;
+            const float *src = base + min(sp0 + j, last) * stride;
             ml[j] = *reinterpret_cast<const float2 *>(src + D);
 #pragma unroll
             for (int k = 0; k < PER; k++) dv[j][k] = src[lane + 64 * k];
@@ -71,6 +78,8 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
             for (int k = 0; k < PER; k++) acc[k] += dv[j][k] * wgt;
         }
     }
+    const int nb = min(tok1 - tok0, p.nmax);   // at most max_query_len
+    if (r >= p.M || t >= nb || splits <= 1) return;
     const float inv = 1.0f / lsum;
     T *o = reinterpret_cast<T *>(p.out) + ((size_t)(tok0 + t) * p.Hq + h * p.G + g) * D;
 #pragma unroll
