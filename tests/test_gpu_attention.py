@@ -75,6 +75,11 @@ def check(ref, got, bf16):
     if bf16:
         u = ulps(ref, got)
         assert u <= 5, f"{u} ulps"
+    else:
+        # the reference's Float32 bound, isapprox(y, exact; rtol = 1e-5) (test/ops/tile.jl:240)
+        d = float(np.linalg.norm((ref - got).astype(np.float64)))
+        nrm = max(float(np.linalg.norm(ref.astype(np.float64))), float(np.linalg.norm(got.astype(np.float64))))
+        assert d <= 1e-5 * nrm, f"relative norm err {d / nrm}"
 
 
 @pytest.mark.parametrize("bf16", [False, True])
