@@ -506,3 +506,49 @@ def test_negative_position_reads_as_zero(gpu, n):
                       path=path)
         err = float(np.max(np.abs(ref - out.float().cpu().numpy())))
         assert err <= 2e-2, f"path {path}: max abs err {err}"
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp32"])
+def test_sequences_longer_than_max_query_len(gpu, kind):
+    """Out of contract: query_start_loc gives sequences more tokens than max_query_len. Every
+    kernel takes a sequence's first max_query_len tokens (n_b capped, so no split partial or
+    grid index leaves what the host sized): those rows equal the oracle's (causal), and the
+    rows past them are never written (their NaN sentinels survive)."""
+    bf16 = kind == "bf16"
+    D, P = 128, 16
+    H, KVH = (32, 8) if bf16 else (16, 8)
+    nmax = 8
+    starts, counts = [100, 40, 0, 300], [5, 12, 3, 20]
+    g = rng(2300 + bf16)
+    pages = sum(-(-(s + n) // P) for s, n in zip(starts, counts)) + 2
+    perm = g.permutation(pages) + 1
+    width = max(-(-(s + n) // P) for s, n in zip(starts, counts))
+    bts = np.zeros((len(starts), width), np.int32)
+    off = 0
+    for b, (s, n) in enumerate(zip(starts, counts)):
+        used = -(-(s + n) // P)
+        bts[b, :used] = perm[off:off + used]
+        off += used
+    dt = torch.bfloat16 if bf16 else torch.float32
+    kp, vp = randn(g, pages, KVH, P, D, bf16=bf16), randn(g, pages, KVH, P, D, bf16=bf16)
+    q = randn(g, sum(counts), H, D, bf16=bf16)
+    qsl = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    positions = np.concatenate([np.arange(s, s + n) for s, n in zip(starts, counts)]).astype(np.int32)
+    qd, kd, vd = dev(q, dt), dev(kp, dt), dev(vp, dt)
+    paths = [ti.TI_PATH_AUTO]
+    if bf16:
+        paths += [ti.TI_PATH_DECODE, ti.TI_PATH_PREFILL, ti.TI_PATH_PREFILL_STAGED, ti.TI_PATH_PREFILL_DIRECT,
+                  ti.TI_PATH_PREFILL_PAIRED, ti.TI_PATH_PREFILL_PAIRED16, ti.TI_PATH_PREFILL_PINGPONG]
+    for path in paths:
+        print(f"n_b > max_query_len, {kind} path {path}", flush=True)
+        ws = ti.attention_workspace(BE, qd, kd, num_seqs=len(starts), max_query_len=nmax, path=path)
+        out = torch.full_like(qd, float("nan"))
+        ti.paged_attention_(BE, out, ws, qd, kd, vd, torch.from_numpy(bts).cuda(),
+                            torch.from_numpy(positions).cuda(), 1 / math.sqrt(D), True,
+                            query_start_loc=torch.from_numpy(qsl).cuda(), max_query_len=nmax, path=path)
+        got = out.float().cpu().numpy()
+        for b, (s, n) in enumerate(zip(starts, counts)):
+            lo, k = qsl[b], min(n, nmax)
+            ref = orc.attention(q[lo:lo + k], bts[b], s, 1 / math.sqrt(D), True, kp, vp)
+            check(ref, got[lo:lo + k], bf16)
+            assert np.isnan(got[lo + k:lo + n]).all(), f"path {path}: seq {b} rows past max_query_len written"
