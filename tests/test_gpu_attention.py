@@ -282,7 +282,7 @@ def test_split_shares_by_length(gpu, name):
 # 16 packed rows): contexts either side of the 16-key tile and of the 4-tile minimum split
 # (one split alone writes the output; longer ones merge only the splits that held keys), 16
 # packed rows (G = 2 x 8 tokens), G = 8 x 2 tokens in the uniform layout, head_dim 64 on
-# 64-token pages, and a non-causal multi-token step.
+# 64-token pages, a non-causal multi-token step, and empty sequences (the last one too).
 # name: (starts, counts, use_qsl, dict(KVH, H, D, P, causal))
 F32_BATCHES = {
     "split_edges": ([0, 14, 15, 63, 64, 1000, 4100], [1] * 7, True, dict(KVH=8, H=16)),
@@ -290,6 +290,7 @@ F32_BATCHES = {
     "g8_uniform": ([3000, 17], [2, 2], False, dict(KVH=4, H=32)),
     "d64_p64": ([5000, 60, 191], [1, 1, 1], True, dict(KVH=2, H=8, D=64, P=64)),
     "non_causal": ([700, 33], [4, 4], True, dict(KVH=8, H=32, causal=False)),
+    "empty_sequences": ([0, 900, 0, 60], [0, 3, 1, 0], True, dict(KVH=8, H=16)),
 }
 
 
@@ -302,6 +303,8 @@ def test_fp32_decode_batches(gpu, name):
     nmax = max(counts)
     D = kw.get("D", 128)
     for b, (s, n) in enumerate(zip(starts, counts)):
+        if n == 0:
+            continue
         lo = qsl[b] if use_qsl else b * nmax
         ref = orc.attention(q[lo:lo + n], bts[b], s, 1 / math.sqrt(D), causal, kp, vp)
         check(ref, got[lo:lo + n], False)

@@ -40,7 +40,8 @@ __global__ void __launch_bounds__(256) combine_kernel(DecodeParams p) {
     const size_t first = p.flat ? (size_t)h * p.flat + mt.x : ((size_t)b * p.Hk + h) * p.splits;
     if (!p.flat && p.min_tiles > 0) {
         // only the splits that held keys wrote partials; one alone wrote the output itself
-        const int len = max(p.positions[tok0], 0) + min(tok1 - tok0, p.nmax);
+        const int n = min(tok1 - tok0, p.nmax);   // an empty sequence reads no position
+        const int len = n > 0 ? max(p.positions[tok0], 0) + n : 0;
         splits = f32_active_splits((len + 15) >> 4, p.splits, p.min_tiles).active;
     }
     const int last = max(splits, 1) - 1;   // loads stay inside the sequence's slots
