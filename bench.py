@@ -30,6 +30,7 @@ sys.path.insert(0, os.path.join(ROOT, "tileinfer.jl_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+FP32_PEAK_TFLOPS = 157.3       # MI355X dense fp32 MFMA, TFLOP/s
 
 
 def log(msg):
@@ -355,6 +356,21 @@ def main():
         b1 = 2 * L1 * K1 * D * 4 + 2 * H1 * D * 4
         extra["decode_fp32_qwen3_06b_ctx1024"] = {"us": round(ms1 * 1e3, 2), "GB/s": round(b1 / ms1 / 1e6, 1)}
         del pools1
+        # the fp32 path on a 512-token causal prefill at the same head shape (not a BASELINE
+        # config: the fp32 matrix-core kernel's multi-token mode)
+        n2 = 512
+        k2 = torch.randn((n2 // P, K1, P, D), device="cuda")
+        v2 = torch.randn_like(k2)
+        bt2 = (torch.randperm(n2 // P, generator=gen) + 1).to(torch.int32).cuda()
+        q2 = torch.randn((n2, H1, D), device="cuda")
+        o2 = torch.empty_like(q2)
+        pos2 = torch.arange(n2, dtype=torch.int32, device="cuda")
+        ws2 = ti.attention_workspace(be, q2, k2)
+        ms2 = time_graph(lambda i: ti.attention_(be, o2, ws2, q2, k2, v2, bt2, pos2, scale))
+        tf2 = 4 * D * H1 * (n2 * (n2 + 1) // 2) / (ms2 * 1e-3) / 1e12
+        extra["prefill_fp32_qwen3_06b_512"] = {"us": round(ms2 * 1e3, 2), "TFLOP/s": round(tf2, 1),
+                                               "pct_fp32_mfma_peak": round(100 * tf2 / FP32_PEAK_TFLOPS, 1)}
+        del k2, v2
     if want("verify"):
         sv = decode_setup(16, 4096 + 16, 16, 32, 8, D, P, 2, gen)
         msv = time_graph(lambda i: decode_call(sv, i, scale))

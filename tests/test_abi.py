@@ -83,6 +83,14 @@ def test_workspace_bytes_decode_and_prefill():
     assert ws(_args(dtype=0, num_seqs=32, total_tokens=32), _cache()) == (0, 32 * 8 * 2 * 4 * 130 * 4)
     # fp32 with 8-token pages runs the VALU kernel: 1024 query waves need no splits
     assert ws(_args(dtype=0, num_seqs=32, total_tokens=32), _cache(page_size=8)) == (0, 0)
+    # fp32 multi-token steps: 16-row q-tiles are work-groups too. One sequence of 4 tokens at
+    # G = 4 is one q-tile (8 items -> 32 splits); a 512-token prefill (128 q-tiles per KV
+    # head) and the verify shape (16 seqs x 4 q-tiles) fill 512 work-groups unsplit.
+    assert ws(_args(dtype=0, num_seqs=1, max_query_len=4, total_tokens=4), _cache()) == (0, 8 * 32 * 16 * 130 * 4)
+    assert ws(_args(dtype=0, num_seqs=1, max_query_len=512, total_tokens=512), _cache()) == (0, 0)
+    assert ws(_args(dtype=0, num_seqs=16, max_query_len=16, total_tokens=256), _cache()) == (0, 0)
+    # two 16-token sequences at G = 4: 2 x 8 x 4 = 64 items -> 8 splits of 64 rows each
+    assert ws(_args(dtype=0, num_seqs=2, max_query_len=16, total_tokens=32), _cache()) == (0, 2 * 8 * 8 * 64 * 130 * 4)
     # independent of context length / pool size: same for a larger pool
     assert ws(_args(), _cache(num_pages=100000))[1] == ws(_args(), _cache())[1]
 

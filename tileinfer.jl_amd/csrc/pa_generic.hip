@@ -128,12 +128,13 @@ __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) 
     }
 }
 
-// Float32 decode on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 products and
+// Float32 attention on the fp32 matrix cores (v_mfma_f32_16x16x4_f32: fp32 products and
 // sums, within the fp32 path's 1e-4 tolerance), for dense fp32 pools with 16-key tiles in one
-// page (P a power of two >= 16), D = 64 or 128 and at most 16 packed query rows (g + G t, as
-// the bf16 decode kernel). Work-group = (key split, KV head, sequence), four waves taking every
-// fourth 16-key tile of the split. Per tile and wave (lane l: row r16 = l % 16, k-group kg =
-// l / 16):
+// page (P a power of two >= 16) and D = 64 or 128: decode, prefill and multi-token steps.
+// Packed query rows g + G t (as the bf16 kernels) form q-tiles of 16 rows. Work-group = (key
+// split, q-tile, KV head, sequence); its keys end after the q-tile's last token (causal), and
+// four waves take every fourth 16-key tile of the split. Per tile and wave (lane l: row r16 =
+// l % 16 of the q-tile, k-group kg = l / 16):
 //   S^T = K Q^T     D/4 MFMAs; MFMA (j, c) sums head-dim elements 16 j + 4 kg' + c over kg'
 //                   (lane: key r16's and row r16's element 16 j + 4 kg + c, from float4 loads);
 //                   the lane gets its row's scores of keys 4 kg + e.
@@ -143,13 +144,16 @@ __global__ void __launch_bounds__(64) generic_attention_kernel(GenericParams p) 
 //                   coalesced row read), B = the lane's probability of key 4 kg + e.
 // The waves merge through LDS; one split writes the output, more write Float32 partials in
 // the decode kernel's layout for the combine kernel.
-struct F32DecodeParams {
+struct F32Params {
     const float *q;
     float *out;
     const float *kp, *vp;
     const int32_t *positions, *qsl, *bt;
     float *part;
     int bt_stride, num_pages, P, pshift, Hk, Hq, G, nmax, M, splits, causal;
+    int B, qtiles;   // sequences; 16-row q-tiles per (sequence, KV head)
+    int sshift;      // log2(splits)
+    int xcd;         // 1-D grid, work-groups of one (sequence, KV head) on one XCD (pairs % 8 == 0)
     float scale_log2;
 };
 
@@ -157,25 +161,46 @@ struct F32DecodeParams {
 // fewer work-groups than the launch holds.
 constexpr int F32_MIN_TILES = 4;
 
-template <int D>
-__global__ void __launch_bounds__(256) decode_f32_kernel(F32DecodeParams p) {
+template <int D, bool QT>   // QT: more than one q-tile per (sequence, KV head)
+__global__ void __launch_bounds__(256) attn_f32_kernel(F32Params p) {
     constexpr int NJ = D / 16, NDB = D / 16, NW = 4, MROW = D + 4;
     __shared__ __attribute__((aligned(16))) float slab[NW * 16 * MROW];
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r16 = lane & 15, kg = lane >> 4;
-    const int s = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    // Work item: key split s, q-tile qt, KV head h, sequence b. Grid (splits x q-tiles, Hk, B),
+    // or with xcd a 1-D grid: work-groups are dealt to the 8 XCDs round-robin by index, so
+    // the items of one (sequence, KV head) pair take indices that share their residue mod 8,
+    // run on one XCD and read the pair's keys and values through one L2.
+    int item, h, b;
+    if (QT && p.xcd) {
+        const int QX = p.splits * p.qtiles, k = blockIdx.x >> 3;
+        const int pair = (int)(blockIdx.x & 7) + 8 * (k / QX);
+        item = k % QX;
+        h = pair % p.Hk;
+        b = pair / p.Hk;
+    } else {
+        item = blockIdx.x;
+        h = blockIdx.y;
+        b = blockIdx.z;
+    }
+    const int s = QT ? item & (p.splits - 1) : item, qt = QT ? item >> p.sshift : 0;
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
     const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
-    if (nb <= 0) return;
+    const int t_first = QT ? 16 * qt / p.G : 0;
+    if (t_first >= nb) return;   // the q-tile holds no token of this sequence
     const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
+    // splits cut the sequence's 16-key tiles (the combine derives the same count); this
+    // q-tile's keys end after its last token's position
     const ActiveSplits as = f32_active_splits((len + 15) >> 4, p.splits, F32_MIN_TILES);
     if (s >= as.active) return;   // no keys for this split
-    const int j0 = s * as.per, j1 = min(j0 + as.per, (len + 15) >> 4);
-    const int t = r16 / p.G, g = r16 - t * p.G;
-    const bool ok = r16 < p.M && t < nb;
+    const int t_last = QT ? min((16 * qt + 15) / p.G, nb - 1) : nb - 1;
+    const int kend = p.causal ? start + t_last + 1 : len;
+    const int j0 = s * as.per, j1 = min(j0 + as.per, (kend + 15) >> 4);   // may be empty: (m, l) = (NEG_BIG, 0)
+    const int r = 16 * qt + r16, t = r / p.G, g = r - t * p.G;
+    const bool ok = r < p.M && t < nb;
     const int qpos = p.causal && ok ? start + t : len - 1;
-    const int mask_from = p.causal ? start : len - 1;   // keys up to here are visible to every row
+    const int mask_from = p.causal ? start + t_first : len - 1;   // keys up to here are visible to every row
     f32x4 qv[NJ];
     {
         const float *qr = p.q + ((size_t)(tok0 + (ok ? t : 0)) * p.Hq + h * p.G + g) * D + 4 * kg;
@@ -252,16 +277,18 @@ __global__ void __launch_bounds__(256) decode_f32_kernel(F32DecodeParams p) {
     }
     __syncthreads();
     const size_t unit = ((size_t)b * p.Hk + h) * p.splits + s;
-    for (int item = threadIdx.x; item < p.M * (D / 4); item += NW * 64) {
-        const int r = item / (D / 4), d4 = (item % (D / 4)) * 4;
+    const int mrows = QT ? 16 : p.M;   // one q-tile: the M <= 16 rows
+    for (int it = threadIdx.x; it < mrows * (D / 4); it += NW * 64) {
+        const int rr = it / (D / 4), d4 = (it % (D / 4)) * 4, r = 16 * qt + rr;
+        if (r >= p.M) continue;
         float mx = NEG_BIG;
 #pragma unroll
-        for (int wi = 0; wi < NW; wi++) mx = fmaxf(mx, slab[((size_t)wi * 16 + r) * MROW + D]);
+        for (int wi = 0; wi < NW; wi++) mx = fmaxf(mx, slab[((size_t)wi * 16 + rr) * MROW + D]);
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         float lsum = 0.0f;
 #pragma unroll
         for (int wi = 0; wi < NW; wi++) {
-            const float *src = slab + ((size_t)wi * 16 + r) * MROW;
+            const float *src = slab + ((size_t)wi * 16 + rr) * MROW;
             const float wgt = fast_exp2(src[D] - mx);
             lsum += src[D + 1] * wgt;
             acc += *reinterpret_cast<const f32x4 *>(src + d4) * wgt;
@@ -291,20 +318,22 @@ void launch(const GenericParams &p, int D, dim3 grid, hipStream_t s) {
 
 }  // namespace
 
-// fp32 steps that the matrix-core decode kernel takes: dense fp32 pools, pages of 2^k >= 16
-// tokens, D = 64 or 128, at most 16 packed query rows. Its key splits: while the (sequence,
-// KV head) pairs times splits are fewer than F32_TARGET work-groups, double (at most 32);
-// short contexts then use fewer of them (F32_MIN_TILES).
+// fp32 steps that the matrix-core kernel takes: dense fp32 pools, pages of 2^k >= 16 tokens,
+// D = 64 or 128. Its key splits: while the (sequence, KV head, q-tile) items times splits are
+// fewer than F32_TARGET work-groups, double (at most 32); short contexts then use fewer of
+// them (F32_MIN_TILES).
 constexpr int F32_TARGET = 512, F32_MAX_SPLITS = 32;
 static bool f32_mfma(const ti_attention_args *a, const ti_kv_cache *c) {
-    const int G = a->q_heads / c->kv_heads;
     return a->dtype == TI_F32 && c->kind == TI_KV_DENSE && (c->head_dim == 64 || c->head_dim == 128) &&
-           c->page_size >= 16 && (c->page_size & (c->page_size - 1)) == 0 && G * a->max_query_len <= 16;
+           c->page_size >= 16 && (c->page_size & (c->page_size - 1)) == 0;
+}
+static int f32_qtiles(const ti_attention_args *a, const ti_kv_cache *c) {
+    return (a->q_heads / c->kv_heads * a->max_query_len + 15) / 16;
 }
 static int f32_splits(const ti_attention_args *a, const ti_kv_cache *c) {
-    const long long pairs = (long long)a->num_seqs * c->kv_heads;
+    const long long items = (long long)a->num_seqs * c->kv_heads * f32_qtiles(a, c);
     int sp = 1;
-    while (sp < F32_MAX_SPLITS && pairs * sp < F32_TARGET) sp <<= 1;
+    while (sp < F32_MAX_SPLITS && items * sp < F32_TARGET) sp <<= 1;
     return sp;
 }
 
@@ -327,7 +356,7 @@ int ti_plan_generic(const ti_attention_args *a, const ti_kv_cache *c, size_t *by
 
 int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStream_t s) {
     if (f32_mfma(a, c)) {
-        F32DecodeParams f;
+        F32Params f;
         f.q = (const float *)a->q;
         f.out = (float *)a->out;
         f.kp = (const float *)c->k_pages;
@@ -350,9 +379,21 @@ int ti_launch_generic(const ti_attention_args *a, const ti_kv_cache *c, hipStrea
         f.splits = ti_plan_generic(a, c, &bytes);
         if (bytes > 0 && (!a->workspace || a->workspace_bytes < bytes)) f.splits = 1;   // runs unsplit
         f.part = (float *)a->workspace;
-        const dim3 grid(f.splits, c->kv_heads, a->num_seqs);
-        if (c->head_dim == 128) decode_f32_kernel<128><<<grid, 256, 0, s>>>(f);
-        else decode_f32_kernel<64><<<grid, 256, 0, s>>>(f);
+        f.B = a->num_seqs;
+        f.qtiles = f32_qtiles(a, c);
+        const long long pairs = (long long)a->num_seqs * c->kv_heads;
+        const long long wgs = pairs * f.qtiles * f.splits;
+        if (wgs > 0x7fffffffLL) return TI_ERR_UNSUPPORTED;
+        f.sshift = __builtin_ctz(f.splits);
+        f.xcd = pairs % 8 == 0 && f.qtiles > 1;   // decode (one q-tile) reuses no tile across work-groups
+        const dim3 grid = f.xcd ? dim3((unsigned)wgs) : dim3((unsigned)(f.splits * f.qtiles), c->kv_heads, a->num_seqs);
+        if (f.qtiles > 1) {
+            if (c->head_dim == 128) attn_f32_kernel<128, true><<<grid, 256, 0, s>>>(f);
+            else attn_f32_kernel<64, true><<<grid, 256, 0, s>>>(f);
+        } else {
+            if (c->head_dim == 128) attn_f32_kernel<128, false><<<grid, 256, 0, s>>>(f);
+            else attn_f32_kernel<64, false><<<grid, 256, 0, s>>>(f);
+        }
         if (hipGetLastError() != hipSuccess) return TI_ERR_LAUNCH;
         return f.splits > 1 ? ti_launch_combine(a, c, f.M, f.splits, s, 0, nullptr, F32_MIN_TILES) : TI_OK;
     }
