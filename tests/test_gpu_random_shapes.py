@@ -2,8 +2,9 @@
 
 Each case draws head_dim, heads per KV head, page size, cached prefix, query count,
 causality and cache type, builds a fragmented block table, and compares the GPU output
-with the double-accumulated oracle: max abs <= 2e-2 (bf16, INT8-KV) or <= 1e-4 (fp32, and
-the reference's relative 2-norm bound 1e-5).
+with the double-accumulated oracle: max abs <= 2e-2 (bf16), <= 2e-2 + one bf16 unit of the
+reference value and <= 14 ulps (INT8-KV), or <= 1e-4 (fp32, and the reference's relative
+2-norm bound 1e-5).
 The case parameters are printed before each call so a failure names its shape.
 TI_RANDOM_SHAPES sets the number of cases (default 60)."""
 import math
@@ -14,7 +15,7 @@ import pytest
 import torch
 
 import tileinfer_hip as ti
-from helpers import block_table, randn, rng, smoothing
+from helpers import block_table, randn, rng, smoothing, ulps
 from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
@@ -85,8 +86,20 @@ def test_random_shape(gpu, seed):
         ws = ti.attention_workspace(BE, qd, k, path=path)
         ti.attention_(BE, out, ws, qd, k, v, btd, pos, scale, causal, path=path)
         got = out.float().cpu().numpy()
-        err = float(np.max(np.abs(ref - got)))
-        assert err <= tol, f"path {path}: max abs err {err}"
+        if kind == "int8":
+            # INT8: 2e-2 plus one bf16 unit of the reference value (the output's own rounding),
+            # and the reference's INT8 bound of 14 ulps (test/ops/tile.jl:256). Its algorithm
+            # rounds p * s_v to bf16, so where outputs reach |o| ~ 2.4 the exact result is out of
+            # a flat 2e-2 at times: seed 18373, 1 case in ~4500, 0.021 at o = -2.354 on every
+            # prefill kernel alike (10 ulps), where the reference's own eager op is 0.018 off
+            # (27 ulps) on the same inputs.
+            excess = float(np.max(np.abs(ref - got) - (tol + np.abs(ref) * 2.0 ** -8)))
+            assert excess <= 0, f"path {path}: abs err over 2e-2 + |ref| 2^-8 by {excess}"
+            u = ulps(ref, got)
+            assert u <= 14, f"path {path}: {u} ulps"
+        else:
+            err = float(np.max(np.abs(ref - got)))
+            assert err <= tol, f"path {path}: max abs err {err}"
         if kind == "fp32":
             # the reference's Float32 bound, isapprox(y, exact; rtol = 1e-5) (test/ops/tile.jl:240)
             d = float(np.linalg.norm((ref - got).astype(np.float64)))

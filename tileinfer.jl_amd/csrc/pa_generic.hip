@@ -184,7 +184,14 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(F32Params p) {
         h = blockIdx.y;
         b = blockIdx.z;
     }
-    const int s = QT ? item & (p.splits - 1) : item, qt = QT ? item >> p.sshift : 0;
+    // q-tiles in fold order (the heavier causal half descending, then the lighter half
+    // ascending), so the work-groups a CU holds together pair a heavy and a light q-tile
+    const int s = QT ? item & (p.splits - 1) : item;
+    int qt = 0;
+    if (QT) {
+        const int u = item >> p.sshift, half = (p.qtiles + 1) >> 1;
+        qt = u < half ? p.qtiles - 1 - u : u - half;
+    }
     const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
     const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
     const int t_first = QT ? 16 * qt / p.G : 0;
@@ -213,26 +220,31 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(F32Params p) {
     for (int db = 0; db < NDB; db++) o[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
     float m = NEG_BIG, l = 0.0f;
     const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
-    for (int j = j0 + w; j < j1; j += NW) {
+    struct Tile {
+        f32x4 k[NJ];
+        float v[4][NDB];
+    };
+    auto load = [&](int j, Tile &tl) {
         const int pos0 = j * 16, last = len - 1 - pos0;   // keys past len read the last key's row
         const int pg = page_of_s(bt, pos0 >> p.pshift, p.bt_stride, p.num_pages);
         const long long rbase = ((long long)pg * p.Hk + h) * p.P + (pos0 & (p.P - 1));
         const float *krow = p.kp + (rbase + min(r16, last)) * D + 4 * kg;
-        f32x4 kv[NJ];
 #pragma unroll
-        for (int jj = 0; jj < NJ; jj++) kv[jj] = *reinterpret_cast<const f32x4 *>(krow + 16 * jj);
-        float vv[4][NDB];
+        for (int jj = 0; jj < NJ; jj++) tl.k[jj] = *reinterpret_cast<const f32x4 *>(krow + 16 * jj);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const float *vrow = p.vp + (rbase + min(4 * kg + e, last)) * D + r16;
 #pragma unroll
-            for (int db = 0; db < NDB; db++) vv[e][db] = vrow[16 * db];
+            for (int db = 0; db < NDB; db++) tl.v[e][db] = vrow[16 * db];
         }
+    };
+    auto compute = [&](int j, const Tile &tl) {
+        const int pos0 = j * 16;
         f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int jj = 0; jj < NJ; jj++)
 #pragma unroll
-            for (int c = 0; c < 4; c++) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[jj][c], qv[jj][c], sc, 0, 0, 0);
+            for (int c = 0; c < 4; c++) sc = __builtin_amdgcn_mfma_f32_16x16x4f32(tl.k[jj][c], qv[jj][c], sc, 0, 0, 0);
         const bool need_mask = pos0 + 15 > mask_from;
         float x[4], mt = -INFINITY;
 #pragma unroll
@@ -261,7 +273,33 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(F32Params p) {
 #pragma unroll
         for (int e = 0; e < 4; e++)
 #pragma unroll
-            for (int db = 0; db < NDB; db++) o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[e][db], pe[e], o[db], 0, 0, 0);
+            for (int db = 0; db < NDB; db++) o[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(tl.v[e][db], pe[e], o[db], 0, 0, 0);
+    };
+    if constexpr (QT) {
+        // multi-token q-tiles walk many tiles per wave: the next tile's loads are issued
+        // before this one's arithmetic (two register sets; past the last tile the prefetch
+        // re-reads it, unused)
+        Tile ta, tb;
+        int j = j0 + w;
+        if (j < j1) {
+            load(j, ta);
+            while (true) {
+                load(min(j + NW, j1 - 1), tb);
+                compute(j, ta);
+                j += NW;
+                if (j >= j1) break;
+                load(min(j + NW, j1 - 1), ta);
+                compute(j, tb);
+                j += NW;
+                if (j >= j1) break;
+            }
+        }
+    } else {
+        for (int j = j0 + w; j < j1; j += NW) {
+            Tile tl;
+            load(j, tl);
+            compute(j, tl);
+        }
     }
     // merge the four waves' states (same rows, disjoint keys) through LDS
     l += __shfl_xor(l, 16);
