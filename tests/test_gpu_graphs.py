@@ -105,8 +105,8 @@ def test_prefill_and_kv_write_graph(gpu, path, n):
 
 def _pools(kind, pages, Hk, P, D):
     """Two identical caches (random contents stand for the cached prefix)."""
-    if kind == "bf16":
-        k = torch.randn((pages, Hk, P, D), device="cuda", dtype=torch.bfloat16)
+    if kind in ("bf16", "fp32"):
+        k = torch.randn((pages, Hk, P, D), device="cuda", dtype=torch.bfloat16 if kind == "bf16" else torch.float32)
         v = torch.randn_like(k)
         return (k, v), (k.clone(), v.clone())
     kq, vq = ti.int8_kv_pools(D, P, Hk, pages, torch.rand(D) + 0.5)
@@ -122,7 +122,8 @@ def _pool_tensors(kv):
     return (k.layer_q, k.layer_scale) if isinstance(k, ti.Int8Pages) else (k, v)
 
 
-@pytest.mark.parametrize("B,n,kind", [(4, 1, "bf16"), (2, 16, "bf16"), (1, 64, "bf16"), (4, 1, "int8")])
+@pytest.mark.parametrize("B,n,kind", [(4, 1, "bf16"), (2, 16, "bf16"), (1, 64, "bf16"), (4, 1, "int8"),
+                                      (4, 1, "fp32"), (2, 16, "fp32")])
 def test_runner_step_graph_with_block_table_rewrites(gpu, B, n, kind):
     """The reference's runner step (src/model/decoder.jl:137-196, test/engine/runner.jl:
     16-33): pages are reserved from a shared BlockManager as the sequences grow, so new
@@ -144,10 +145,11 @@ def test_runner_step_graph_with_block_table_rewrites(gpu, B, n, kind):
         ti.reserve(bm, seqs[b], L)
         seqs[b].tokens.extend([0] * L)
     cache, eager = _pools(kind, pages, Hk, P, D)
-    table = ti.RotaryTable.build(D, 2048, 1e6, torch.bfloat16)
+    dt = torch.float32 if kind == "fp32" else torch.bfloat16
+    table = ti.RotaryTable.build(D, 2048, 1e6, dt)
     T = B * n
-    qkv = torch.empty((T, (Hq + 2 * Hk) * D), device="cuda", dtype=torch.bfloat16)
-    q = torch.empty((T, Hq, D), device="cuda", dtype=torch.bfloat16)
+    qkv = torch.empty((T, (Hq + 2 * Hk) * D), device="cuda", dtype=dt)
+    q = torch.empty((T, Hq, D), device="cuda", dtype=dt)
     out = torch.empty_like(q)
     staging = torch.zeros(2 * T + B * width, dtype=torch.int32, device="cuda")
     pos = torch.zeros(T, dtype=torch.int32, device="cuda")
@@ -201,7 +203,7 @@ def test_runner_step_graph_with_block_table_rewrites(gpu, B, n, kind):
         assert torch.equal(got, ref_out), f"replay {it} attention differs from eager"
         for a, e in zip(_pool_tensors(cache), _pool_tensors(eager)):
             assert torch.equal(a, e), f"replay {it} cache differs from eager"
-        if kind == "bf16":
+        if kind != "int8":
             # sequence 0's attention against the oracle over the cache the step wrote
             s = seqs[0]
             start = len(s) - n
@@ -209,5 +211,5 @@ def test_runner_step_graph_with_block_table_rewrites(gpu, B, n, kind):
             ref = orc.attention(q[:n].float().cpu().numpy(), np.array(s.block_table, np.int32), start,
                                 scale, True, kp, vp)
             err = float(np.max(np.abs(ref - got[:n].float().cpu().numpy())))
-            assert err <= 2e-2, f"replay {it}: max abs err {err} vs oracle"
+            assert err <= (2e-2 if kind == "bf16" else 1e-4), f"replay {it}: max abs err {err} vs oracle"
     assert grew > 0, "no step reserved a new page"
