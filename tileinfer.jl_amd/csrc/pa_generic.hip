@@ -185,7 +185,8 @@ __global__ void __launch_bounds__(256) attn_f32_kernel(F32Params p) {
         b = blockIdx.z;
     }
     // q-tiles in fold order (the heavier causal half descending, then the lighter half
-    // ascending), so the work-groups a CU holds together pair a heavy and a light q-tile
+    // ascending): work-groups dispatched half a round apart, which tend to share a CU, then
+    // pair a heavy and a light q-tile (a placement hint only; any order is correct)
     const int s = QT ? item & (p.splits - 1) : item;
     int qt = 0;
     if (QT) {
