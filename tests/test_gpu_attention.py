@@ -118,6 +118,15 @@ def test_attention_limits(gpu, case):
     check(ref, run_gpu(c, torch.bfloat16, ti.TI_PATH_PREFILL), True)
 
 
+@pytest.mark.parametrize("case", [LIMIT_CASES[0], LIMIT_CASES[1], LIMIT_CASES[2], LIMIT_CASES[4]], ids=str)
+def test_attention_limits_fp32(gpu, case):
+    """The fp32 matrix-core kernel at the largest shapes: a 128k-token context (32 key splits),
+    64 query heads per KV head (4 q-tiles per token), and a 16-query step on a 64k context."""
+    print(f"case {case}", flush=True)
+    c = make_case(case, False, seed=hash(case) % 10000 + 13)
+    check(exact(c), run_gpu(c, torch.float32), False)
+
+
 @pytest.mark.parametrize("case", REF_CASES + EXTRA_CASES[:5], ids=str)
 def test_attention_int8(gpu, case):
     """INT8 cache (bf16 activations), keys scaled like the smoothing factors."""
