@@ -413,6 +413,22 @@ def main():
                                                         positions, slots_t, 1e-6))
         kb = (n * (Hq + 2 * Hk) * D * 2) + (n * Hq * D * 2) + 2 * n * Hk * D * 2 + n * 2 * D * 2
         extra["rope_kv_write_512"] = {"us": round(msk * 1e3, 2), "GB/s": round(kb / msk / 1e6, 1)}
+        # the unfused ops of the same step (the reference's generic chain): store_kv into
+        # dense bf16 and INT8 pages, and rope on the queries
+        kk = torch.randn((n, Hk, D), device="cuda", dtype=torch.bfloat16)
+        vv = torch.randn_like(kk)
+        mss = time_graph(lambda i: ti.store_kv_(be, kpool, vpool, kk, vv, slots_t))
+        sb = 2 * n * Hk * D * 2 * 2 + n * 4                       # read k, v; write both; slots
+        extra["store_kv_bf16_512"] = {"us": round(mss * 1e3, 2), "GB/s": round(sb / mss / 1e6, 1)}
+        kq, vq = ti.int8_kv_pools(D, P, Hk, 64 + 32)
+        msq = time_graph(lambda i: ti.store_kv_(be, kq, vq, kk, vv, slots_t))
+        qb = 2 * n * Hk * D * 2 + 2 * n * Hk * (D + 4) + n * 4    # read bf16 k, v; write int8 + scales
+        extra["store_kv_int8_512"] = {"us": round(msq * 1e3, 2), "GB/s": round(qb / msq / 1e6, 1)}
+        xr = torch.randn((n, Hq, D), device="cuda", dtype=torch.bfloat16)
+        yr = torch.empty_like(xr)
+        msr = time_graph(lambda i: ti.rope_(be, yr, xr, table.cos, table.sin, positions))
+        rb = 2 * n * Hq * D * 2 + n * 2 * D * 2 + n * 4           # read x, write y; cos, sin rows
+        extra["rope_q_512"] = {"us": round(msr * 1e3, 2), "GB/s": round(rb / msr / 1e6, 1)}
 
     result = {
         "metric": "decode attn GB/s (% of HBM peak) & prefill attn TFLOP/s at Qwen3-4B shape",
