@@ -421,6 +421,10 @@ def main():
         sb = 2 * n * Hk * D * 2 * 2 + n * 4                       # read k, v; write both; slots
         extra["store_kv_bf16_512"] = {"us": round(mss * 1e3, 2), "GB/s": round(sb / mss / 1e6, 1)}
         kq, vq = ti.int8_kv_pools(D, P, Hk, 64 + 32)
+        msf = time_graph(lambda i: ti.attention_inputs_(be, qo, kq, vq, qkv, None, None, table,
+                                                        positions, slots_t, 1e-6))
+        fb = (n * (Hq + 2 * Hk) * D * 2) + (n * Hq * D * 2) + 2 * n * Hk * (D + 4) + n * 2 * D * 2
+        extra["rope_kv_write_int8_512"] = {"us": round(msf * 1e3, 2), "GB/s": round(fb / msf / 1e6, 1)}
         msq = time_graph(lambda i: ti.store_kv_(be, kq, vq, kk, vv, slots_t))
         qb = 2 * n * Hk * D * 2 + 2 * n * Hk * (D + 4) + n * 4    # read bf16 k, v; write int8 + scales
         extra["store_kv_int8_512"] = {"us": round(msq * 1e3, 2), "GB/s": round(qb / msq / 1e6, 1)}

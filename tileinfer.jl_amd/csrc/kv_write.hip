@@ -249,6 +249,27 @@ __global__ void __launch_bounds__(64) attention_inputs_kernel(
     }
 }
 
+// quantize_store for one vector held by a 16-lane group, 8 elements per lane: elements
+// x[0..3] go to bytes o1 .. o1 + 3 of the row, x[4..7] to o2 .. o2 + 3 (as 32-bit words).
+__device__ __forceinline__ void quantize16(const float (&x)[8], int8_t *__restrict__ qrow, int o1,
+                                           int o2, float *__restrict__ scale, int u) {
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) m = fmaxf(m, fabsf(x[e]));
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float inv = m > 0.0f ? __fdiv_rn(127.0f, m) : 0.0f;
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int qv = (int)floorf(__fadd_rn(__fmul_rn(x[e], inv), 0.5f));
+        w[e >> 2] |= (uint32_t)(uint8_t)(int8_t)qv << (8 * (e & 3));
+    }
+    *reinterpret_cast<uint32_t *>(qrow + o1) = w[0];
+    *reinterpret_cast<uint32_t *>(qrow + o2) = w[1];
+    if (u == 0) *scale = __fdiv_rn(m, 127.0f);
+}
+
 // Vectorized form of attention_inputs_kernel for dense caches with head_dim 128: 16 lanes
 // per head, lane u owning elements 4u .. 4u + 3 of each half (8-byte bf16 / 16-byte
 // Float32 loads), 16 heads per 256-thread work-group: grid (n, ceil((nq + nkv) / 16)).
@@ -282,9 +303,13 @@ template <> struct Vec4<float> {
     }
 };
 
-template <typename T, bool NORM>
+// INT8 caches: a KV head's 16 lanes reduce the absmax of its 128 (smoothed) key or value
+// elements with four xor shuffles and each lane stores its quantized elements as 32-bit words;
+// the arithmetic is quantize_store's element by element (bit-identical).
+template <typename T, bool NORM, bool INT8>
 __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
-    T *__restrict__ q_out, T *__restrict__ kp, T *__restrict__ vp, const T *__restrict__ qkv,
+    T *__restrict__ q_out, T *__restrict__ kp, T *__restrict__ vp, int8_t *__restrict__ lq,
+    float *__restrict__ ls, const float *__restrict__ smooth, const T *__restrict__ qkv,
     const T *__restrict__ q_norm, const T *__restrict__ k_norm, const T *__restrict__ cos_sin,
     int table_len, const int32_t *__restrict__ positions, const int32_t *__restrict__ slots,
     int nq, int nkv, int P, int pages, float eps) {
@@ -351,14 +376,51 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
         y1[e] = E::rnd(E::rnd(a[e] * c1[e]) + E::rnd(-b[e] * s1[e]));
         y2[e] = E::rnd(E::rnd(b[e] * c2[e]) + E::rnd(a[e] * s2[e]));
     }
-    T *dst = is_q ? q_out + ((size_t)t * nq + j) * D : kp + (size_t)row * D;
-    V::st(dst + 4 * u, y1);
-    V::st(dst + HALF + 4 * u, y2);
-    if (is_q) return;
-    // the value row (loaded above): a bit copy in 16-byte chunks over the 16 lanes
-    uint4 *vd = reinterpret_cast<uint4 *>(vp + (size_t)row * D);
+    if (!INT8 || is_q) {
+        T *dst = is_q ? q_out + ((size_t)t * nq + j) * D : kp + (size_t)row * D;
+        V::st(dst + 4 * u, y1);
+        V::st(dst + HALF + 4 * u, y2);
+        if (is_q) return;
+    }
+    if constexpr (!INT8) {
+        // the value row (loaded above): a bit copy in 16-byte chunks over the 16 lanes
+        uint4 *vd = reinterpret_cast<uint4 *>(vp + (size_t)row * D);
 #pragma unroll
-    for (int c = 0; c < VCH / 16; c++) vd[u + 16 * c] = vrow[c];
+        for (int c = 0; c < VCH / 16; c++) vd[u + 16 * c] = vrow[c];
+    } else {
+        const size_t half_q = (size_t)pages * nkv * P * D, half_s = (size_t)pages * nkv * P;
+        // keys: the rotated elements 4u + e and 64 + 4u + e divided by their smoothing
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[e] = __fdiv_rn(y1[e], smooth[4 * u + e]);
+            x[4 + e] = __fdiv_rn(y2[e], smooth[HALF + 4 * u + e]);
+        }
+        quantize16(x, lq + (size_t)row * D, 4 * u, HALF + 4 * u, ls + row, u);
+        // values: this lane's 16-byte chunks of the row, elements in order
+        float v[8];
+        if constexpr (sizeof(T) == 2) {
+            // chunk u = elements 8u .. 8u + 7
+            const uint4 w = vrow[0];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[2 * e] = __uint_as_float(ws[e] << 16);
+                v[2 * e + 1] = __uint_as_float(ws[e] & 0xffff0000u);
+            }
+            quantize16(v, lq + half_q + (size_t)row * D, 8 * u, 8 * u + 4, ls + half_s + row, u);
+        } else {
+            // chunks u and u + 16 = elements 4u .. 4u + 3 and 64 + 4u .. 64 + 4u + 3
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                v[4 * c] = __uint_as_float(vrow[c].x);
+                v[4 * c + 1] = __uint_as_float(vrow[c].y);
+                v[4 * c + 2] = __uint_as_float(vrow[c].z);
+                v[4 * c + 3] = __uint_as_float(vrow[c].w);
+            }
+            quantize16(v, lq + half_q + (size_t)row * D, 4 * u, HALF + 4 * u, ls + half_s + row, u);
+        }
+    }
 }
 
 }  // namespace
@@ -416,12 +478,12 @@ static void launch_inputs(void *q_out, const ti_kv_cache *c, const void *qkv, co
                           const void *k_norm, const void *cos_sin, int table_len,
                           const int32_t *positions, const int32_t *slots, int n, int nq,
                           float eps, hipStream_t s) {
-    if (!INT8 && c->head_dim == 128) {
+    if (c->head_dim == 128) {
         dim3 grid(n, (nq + c->kv_heads + 15) / 16);
-        attention_inputs_v_kernel<T, NORM><<<grid, 256, 0, s>>>(
-            (T *)q_out, (T *)c->k_pages, (T *)c->v_pages, (const T *)qkv, (const T *)q_norm,
-            (const T *)k_norm, (const T *)cos_sin, table_len, positions, slots, nq, c->kv_heads,
-            c->page_size, c->num_pages, eps);
+        attention_inputs_v_kernel<T, NORM, INT8><<<grid, 256, 0, s>>>(
+            (T *)q_out, (T *)c->k_pages, (T *)c->v_pages, c->layer_q, c->layer_scale, c->smooth,
+            (const T *)qkv, (const T *)q_norm, (const T *)k_norm, (const T *)cos_sin, table_len,
+            positions, slots, nq, c->kv_heads, c->page_size, c->num_pages, eps);
         return;
     }
     dim3 grid(n, nq + c->kv_heads);
