@@ -423,6 +423,42 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
     }
 }
 
+// store_kv into INT8 pages for head_dim 128 with the fused kernel's layout: 16 lanes per KV
+// head (lane u holds elements 4u .. 4u + 3 and 64 + 4u .. 64 + 4u + 3 of the key and of the
+// value), 16 heads per 256-thread work-group; quantize16 is quantize_store element by element.
+template <typename T>
+__global__ void __launch_bounds__(256) store_kv_int8_v_kernel(int8_t *__restrict__ lq,
+                                                              float *__restrict__ ls,
+                                                              const float *__restrict__ smooth,
+                                                              const T *__restrict__ k,
+                                                              const T *__restrict__ v,
+                                                              const int32_t *__restrict__ slots,
+                                                              int P, int H, int pages) {
+    constexpr int D = 128, HALF = 64;
+    using V = Vec4<T>;
+    const int t = blockIdx.x, h = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
+    if (h >= H) return;   // a whole 16-lane group
+    const size_t src = ((size_t)t * H + h) * D;
+    float ka[4], kb[4], va[4], vb[4];
+    V::ld(k + src + 4 * u, ka);
+    V::ld(k + src + HALF + 4 * u, kb);
+    V::ld(v + src + 4 * u, va);
+    V::ld(v + src + HALF + 4 * u, vb);
+    const long long row = slot_row(slots[t], h, P, H, pages);
+    if (row < 0) return;   // the whole group
+    const size_t half_q = (size_t)pages * H * P * D, half_s = (size_t)pages * H * P;
+    float x[8], y[8];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        x[e] = __fdiv_rn(ka[e], smooth[4 * u + e]);
+        x[4 + e] = __fdiv_rn(kb[e], smooth[HALF + 4 * u + e]);
+        y[e] = va[e];
+        y[4 + e] = vb[e];
+    }
+    quantize16(x, lq + (size_t)row * D, 4 * u, HALF + 4 * u, ls + row, u);
+    quantize16(y, lq + half_q + (size_t)row * D, 4 * u, HALF + 4 * u, ls + half_s + row, u);
+}
+
 }  // namespace
 
 int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int H, float eps,
@@ -452,7 +488,17 @@ int ti_launch_store_kv(int dtype, const ti_kv_cache *c, const void *k, const voi
                        const int32_t *slots, int n, hipStream_t s) {
     dim3 grid(n, c->kv_heads);
     const int D = c->head_dim, P = c->page_size, H = c->kv_heads, pages = c->num_pages;
-    if (c->kind == TI_KV_INT8) {
+    if (c->kind == TI_KV_INT8 && D == 128) {
+        const dim3 vgrid(n, (H + 15) / 16);
+        if (dtype == TI_BF16)
+            store_kv_int8_v_kernel<uint16_t><<<vgrid, 256, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
+                                                                   (const uint16_t *)k, (const uint16_t *)v,
+                                                                   slots, P, H, pages);
+        else
+            store_kv_int8_v_kernel<float><<<vgrid, 256, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
+                                                                (const float *)k, (const float *)v, slots,
+                                                                P, H, pages);
+    } else if (c->kind == TI_KV_INT8) {
         if (dtype == TI_BF16)
             store_kv_int8_kernel<uint16_t><<<grid, 64, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
                                                                (const uint16_t *)k, (const uint16_t *)v,
