@@ -459,6 +459,42 @@ __global__ void __launch_bounds__(256) store_kv_int8_v_kernel(int8_t *__restrict
     quantize16(y, lq + half_q + (size_t)row * D, 4 * u, HALF + 4 * u, ls + half_s + row, u);
 }
 
+// rope for head_dim 128 with the fused kernel's layout: 16 lanes per head (lane u holds
+// pair elements 4u .. 4u + 3 and 64 + 4u .. 64 + 4u + 3), 16 heads per 256-thread
+// work-group; the head's elements load before the position does. Same formula and rounding
+// as rope_kernel; rows at positions outside the table are left untouched.
+template <typename T>
+__global__ void __launch_bounds__(256) rope_v_kernel(T *__restrict__ y, const T *__restrict__ x,
+                                                     const T *__restrict__ cos_t,
+                                                     const T *__restrict__ sin_t, int table_len,
+                                                     const int32_t *__restrict__ positions,
+                                                     int heads) {
+    constexpr int D = 128, HALF = 64;
+    using E = Elt<T>;
+    using V = Vec4<T>;
+    const int t = blockIdx.x, h = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
+    if (h >= heads) return;   // a whole 16-lane group
+    const size_t base = ((size_t)t * heads + h) * D;
+    float a[4], b[4];
+    V::ld(x + base + 4 * u, a);
+    V::ld(x + base + HALF + 4 * u, b);
+    const int p = positions[t];
+    if (p < 0 || p >= table_len) return;
+    const size_t tab = (size_t)p * D;
+    float c1[4], c2[4], s1[4], s2[4], y1[4], y2[4];
+    V::ld(cos_t + tab + 4 * u, c1);
+    V::ld(cos_t + tab + HALF + 4 * u, c2);
+    V::ld(sin_t + tab + 4 * u, s1);
+    V::ld(sin_t + tab + HALF + 4 * u, s2);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        y1[e] = E::rnd(E::rnd(a[e] * c1[e]) + E::rnd(-b[e] * s1[e]));
+        y2[e] = E::rnd(E::rnd(b[e] * c2[e]) + E::rnd(a[e] * s2[e]));
+    }
+    V::st(y + base + 4 * u, y1);
+    V::st(y + base + HALF + 4 * u, y2);
+}
+
 }  // namespace
 
 int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int H, float eps,
@@ -473,6 +509,17 @@ int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows
 int ti_launch_rope(int dtype, void *y, const void *x, const void *cos_t, const void *sin_t,
                    int table_len, const int32_t *positions, int n, int heads, int D,
                    hipStream_t s) {
+    if (D == 128) {
+        const dim3 vgrid(n, (heads + 15) / 16);
+        if (dtype == TI_BF16)
+            rope_v_kernel<uint16_t><<<vgrid, 256, 0, s>>>((uint16_t *)y, (const uint16_t *)x,
+                                                          (const uint16_t *)cos_t, (const uint16_t *)sin_t,
+                                                          table_len, positions, heads);
+        else
+            rope_v_kernel<float><<<vgrid, 256, 0, s>>>((float *)y, (const float *)x, (const float *)cos_t,
+                                                       (const float *)sin_t, table_len, positions, heads);
+        return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
+    }
     dim3 grid(n, (heads * (D / 2) + 255) / 256);
     if (dtype == TI_BF16)
         rope_kernel<uint16_t><<<grid, 256, 0, s>>>((uint16_t *)y, (const uint16_t *)x,
