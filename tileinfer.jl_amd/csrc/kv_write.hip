@@ -495,6 +495,38 @@ __global__ void __launch_bounds__(256) rope_v_kernel(T *__restrict__ y, const T 
     V::st(y + base + HALF + 4 * u, y2);
 }
 
+// Dense store_kv for head_dim 128: 16 lanes per KV head, 16 heads per 256-thread
+// work-group, each lane moving its 16-byte chunks of the key and value rows (bit copies),
+// loaded before the slot is.
+template <typename T>
+__global__ void __launch_bounds__(256) store_kv_v_kernel(T *__restrict__ kp, T *__restrict__ vp,
+                                                         const T *__restrict__ k,
+                                                         const T *__restrict__ v,
+                                                         const int32_t *__restrict__ slots, int P,
+                                                         int H, int pages) {
+    constexpr int D = 128, CH = D * (int)sizeof(T) / 16 / 16;   // 16-byte chunks per lane
+    const int t = blockIdx.x, h = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
+    if (h >= H) return;   // a whole 16-lane group
+    const size_t src = ((size_t)t * H + h) * D;
+    const uint4 *ks = reinterpret_cast<const uint4 *>(k + src);
+    const uint4 *vs = reinterpret_cast<const uint4 *>(v + src);
+    uint4 kc[CH], vc[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        kc[c] = ks[u + 16 * c];
+        vc[c] = vs[u + 16 * c];
+    }
+    const long long row = slot_row(slots[t], h, P, H, pages);
+    if (row < 0) return;   // the whole group
+    uint4 *kd = reinterpret_cast<uint4 *>(kp + (size_t)row * D);
+    uint4 *vd = reinterpret_cast<uint4 *>(vp + (size_t)row * D);
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        kd[u + 16 * c] = kc[c];
+        vd[u + 16 * c] = vc[c];
+    }
+}
+
 }  // namespace
 
 int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows, int H, float eps,
@@ -545,6 +577,16 @@ int ti_launch_store_kv(int dtype, const ti_kv_cache *c, const void *k, const voi
             store_kv_int8_v_kernel<float><<<vgrid, 256, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
                                                                 (const float *)k, (const float *)v, slots,
                                                                 P, H, pages);
+    } else if (c->kind != TI_KV_INT8 && D == 128) {
+        const dim3 vgrid(n, (H + 15) / 16);
+        if (dtype == TI_BF16)
+            store_kv_v_kernel<uint16_t><<<vgrid, 256, 0, s>>>((uint16_t *)c->k_pages, (uint16_t *)c->v_pages,
+                                                              (const uint16_t *)k, (const uint16_t *)v, slots,
+                                                              P, H, pages);
+        else
+            store_kv_v_kernel<float><<<vgrid, 256, 0, s>>>((float *)c->k_pages, (float *)c->v_pages,
+                                                           (const float *)k, (const float *)v, slots, P, H,
+                                                           pages);
     } else if (c->kind == TI_KV_INT8) {
         if (dtype == TI_BF16)
             store_kv_int8_kernel<uint16_t><<<grid, 64, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
