@@ -40,9 +40,10 @@ def test_rope_bit_exact(gpu, bf16, dims):
 
 
 @pytest.mark.parametrize("bf16", [False, True])
-def test_store_kv_bit_exact(gpu, bf16):
-    D, P, H, pages, n = 128, 4, 8, 6, 9
-    g = rng(200 + bf16)
+@pytest.mark.parametrize("D", [128, 64, 96])
+def test_store_kv_bit_exact(gpu, bf16, D):
+    P, H, pages, n = 4, 8, 6, 9
+    g = rng(200 + bf16 + D)
     k, v = randn(g, n, H, D, bf16=bf16), randn(g, n, H, D, bf16=bf16)
     slots = np.array([13, 14, 15, 16, 5, 6, 7, 8, 21], np.int32)
     kp = torch.zeros((pages, H, P, D), dtype=DT[bf16], device="cuda")
@@ -55,9 +56,10 @@ def test_store_kv_bit_exact(gpu, bf16):
 
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("smooth", [False, True])
-def test_store_kv_int8_bit_exact(gpu, bf16, smooth):
-    D, P, H, pages, n = 128, 4, 8, 6, 9
-    g = rng(300 + 2 * bf16 + smooth)
+@pytest.mark.parametrize("D", [128, 64, 96])
+def test_store_kv_int8_bit_exact(gpu, bf16, smooth, D):
+    P, H, pages, n = 4, 8, 6, 9
+    g = rng(300 + 2 * bf16 + smooth + D)
     k, v = randn(g, n, H, D, bf16=bf16), randn(g, n, H, D, bf16=bf16)
     slots = np.array([13, 14, 15, 16, 5, 6, 7, 8, 21], np.int32)
     c = smoothing(g, D) if smooth else np.ones(D, np.float32)

@@ -249,15 +249,16 @@ __global__ void __launch_bounds__(64) attention_inputs_kernel(
     }
 }
 
-// quantize_store for one vector held by a 16-lane group, 8 elements per lane: elements
+// quantize_store for one vector held by an LPH-lane group, 8 elements per lane: elements
 // x[0..3] go to bytes o1 .. o1 + 3 of the row, x[4..7] to o2 .. o2 + 3 (as 32-bit words).
-__device__ __forceinline__ void quantize16(const float (&x)[8], int8_t *__restrict__ qrow, int o1,
-                                           int o2, float *__restrict__ scale, int u) {
+template <int LPH>
+__device__ __forceinline__ void quantize_group(const float (&x)[8], int8_t *__restrict__ qrow, int o1,
+                                               int o2, float *__restrict__ scale, int u) {
     float m = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e++) m = fmaxf(m, fabsf(x[e]));
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    for (int o = LPH / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     const float inv = m > 0.0f ? __fdiv_rn(127.0f, m) : 0.0f;
     uint32_t w[2] = {0u, 0u};
 #pragma unroll
@@ -270,9 +271,9 @@ __device__ __forceinline__ void quantize16(const float (&x)[8], int8_t *__restri
     if (u == 0) *scale = __fdiv_rn(m, 127.0f);
 }
 
-// Vectorized form of attention_inputs_kernel for dense caches with head_dim 128: 16 lanes
-// per head, lane u owning elements 4u .. 4u + 3 of each half (8-byte bf16 / 16-byte
-// Float32 loads), 16 heads per 256-thread work-group: grid (n, ceil((nq + nkv) / 16)).
+// Vectorized form of attention_inputs_kernel for head_dim 128 or 64: D / 8 lanes per head
+// (16 or 8), lane u owning elements 4u .. 4u + 3 of each half (8-byte bf16 / 16-byte Float32
+// loads), 2048 / D heads per 256-thread work-group: grid (n, ceil((nq + nkv) / (2048 / D))).
 // Same rounding points element by element. With the q/k norm, each lane keeps the four
 // per-lane partials a_i^2 + b_i^2 (i = 4u + e) that the one-wave kernel's lanes hold and
 // combines them in that kernel's butterfly order (xor 32, 16, 8, 4 across lanes u ^ 8,
@@ -303,20 +304,20 @@ template <> struct Vec4<float> {
     }
 };
 
-// INT8 caches: a KV head's 16 lanes reduce the absmax of its 128 (smoothed) key or value
-// elements with four xor shuffles and each lane stores its quantized elements as 32-bit words;
+// INT8 caches: a KV head's D / 8 lanes reduce the absmax of its D (smoothed) key or value
+// elements with xor shuffles and each lane stores its quantized elements as 32-bit words;
 // the arithmetic is quantize_store's element by element (bit-identical).
-template <typename T, bool NORM, bool INT8>
+template <typename T, bool NORM, bool INT8, int D>
 __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
     T *__restrict__ q_out, T *__restrict__ kp, T *__restrict__ vp, int8_t *__restrict__ lq,
     float *__restrict__ ls, const float *__restrict__ smooth, const T *__restrict__ qkv,
     const T *__restrict__ q_norm, const T *__restrict__ k_norm, const T *__restrict__ cos_sin,
     int table_len, const int32_t *__restrict__ positions, const int32_t *__restrict__ slots,
     int nq, int nkv, int P, int pages, float eps) {
-    constexpr int D = 128, HALF = 64;
+    constexpr int HALF = D / 2, LPH = D / 8, HPW = 256 / LPH;   // lanes, heads per work-group
     using E = Elt<T>;
     using V = Vec4<T>;
-    const int t = blockIdx.x, j = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
+    const int t = blockIdx.x, j = blockIdx.y * HPW + threadIdx.x / LPH, u = threadIdx.x % LPH;
     if (j >= nq + nkv) return;   // a whole 16-lane group
     const bool is_q = j < nq;
     const int h = j - nq;
@@ -330,11 +331,11 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
     V::ld(qkv + col + 4 * u, a);
     V::ld(qkv + col + HALF + 4 * u, b);
     constexpr int VCH = D * (int)sizeof(T) / 16;   // 16-byte chunks of a value row
-    uint4 vrow[VCH / 16];
+    uint4 vrow[VCH / LPH];
     if (!is_q) {
         const uint4 *vs = reinterpret_cast<const uint4 *>(qkv + ((size_t)t * (nq + 2 * nkv) + nq + nkv + h) * D);
 #pragma unroll
-        for (int c = 0; c < VCH / 16; c++) vrow[c] = vs[u + 16 * c];
+        for (int c = 0; c < VCH / LPH; c++) vrow[c] = vs[u + LPH * c];
     }
     float w1[4], w2[4];
     if (NORM) {
@@ -353,7 +354,7 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
 #pragma unroll
         for (int e = 0; e < 4; e++) pp[e] = a[e] * a[e] + b[e] * b[e];
 #pragma unroll
-        for (int o = 8; o > 0; o >>= 1)
+        for (int o = LPH / 2; o > 0; o >>= 1)
 #pragma unroll
             for (int e = 0; e < 4; e++) pp[e] = pp[e] + __shfl_xor(pp[e], o);
         const float p02 = pp[0] + pp[2], p13 = pp[1] + pp[3];
@@ -383,10 +384,10 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
         if (is_q) return;
     }
     if constexpr (!INT8) {
-        // the value row (loaded above): a bit copy in 16-byte chunks over the 16 lanes
+        // the value row (loaded above): a bit copy in 16-byte chunks over the head's lanes
         uint4 *vd = reinterpret_cast<uint4 *>(vp + (size_t)row * D);
 #pragma unroll
-        for (int c = 0; c < VCH / 16; c++) vd[u + 16 * c] = vrow[c];
+        for (int c = 0; c < VCH / LPH; c++) vd[u + LPH * c] = vrow[c];
     } else {
         const size_t half_q = (size_t)pages * nkv * P * D, half_s = (size_t)pages * nkv * P;
         // keys: the rotated elements 4u + e and 64 + 4u + e divided by their smoothing
@@ -396,7 +397,7 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
             x[e] = __fdiv_rn(y1[e], smooth[4 * u + e]);
             x[4 + e] = __fdiv_rn(y2[e], smooth[HALF + 4 * u + e]);
         }
-        quantize16(x, lq + (size_t)row * D, 4 * u, HALF + 4 * u, ls + row, u);
+        quantize_group<LPH>(x, lq + (size_t)row * D, 4 * u, HALF + 4 * u, ls + row, u);
         // values: this lane's 16-byte chunks of the row, elements in order
         float v[8];
         if constexpr (sizeof(T) == 2) {
@@ -408,9 +409,9 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
                 v[2 * e] = __uint_as_float(ws[e] << 16);
                 v[2 * e + 1] = __uint_as_float(ws[e] & 0xffff0000u);
             }
-            quantize16(v, lq + half_q + (size_t)row * D, 8 * u, 8 * u + 4, ls + half_s + row, u);
+            quantize_group<LPH>(v, lq + half_q + (size_t)row * D, 8 * u, 8 * u + 4, ls + half_s + row, u);
         } else {
-            // chunks u and u + 16 = elements 4u .. 4u + 3 and 64 + 4u .. 64 + 4u + 3
+            // chunks u and u + LPH = elements 4u .. 4u + 3 and HALF + 4u .. HALF + 4u + 3
 #pragma unroll
             for (int c = 0; c < 2; c++) {
                 v[4 * c] = __uint_as_float(vrow[c].x);
@@ -418,15 +419,16 @@ __global__ void __launch_bounds__(256) attention_inputs_v_kernel(
                 v[4 * c + 2] = __uint_as_float(vrow[c].z);
                 v[4 * c + 3] = __uint_as_float(vrow[c].w);
             }
-            quantize16(v, lq + half_q + (size_t)row * D, 4 * u, HALF + 4 * u, ls + half_s + row, u);
+            quantize_group<LPH>(v, lq + half_q + (size_t)row * D, 4 * u, HALF + 4 * u, ls + half_s + row, u);
         }
     }
 }
 
-// store_kv into INT8 pages for head_dim 128 with the fused kernel's layout: 16 lanes per KV
-// head (lane u holds elements 4u .. 4u + 3 and 64 + 4u .. 64 + 4u + 3 of the key and of the
-// value), 16 heads per 256-thread work-group; quantize16 is quantize_store element by element.
-template <typename T>
+// store_kv into INT8 pages for head_dim 128 or 64 with the fused kernel's layout: D / 8 lanes
+// per KV head (lane u holds elements 4u .. 4u + 3 and D/2 + 4u .. D/2 + 4u + 3 of the key and
+// of the value), 2048 / D heads per 256-thread work-group; quantize_group is quantize_store
+// element by element.
+template <typename T, int D>
 __global__ void __launch_bounds__(256) store_kv_int8_v_kernel(int8_t *__restrict__ lq,
                                                               float *__restrict__ ls,
                                                               const float *__restrict__ smooth,
@@ -434,9 +436,9 @@ __global__ void __launch_bounds__(256) store_kv_int8_v_kernel(int8_t *__restrict
                                                               const T *__restrict__ v,
                                                               const int32_t *__restrict__ slots,
                                                               int P, int H, int pages) {
-    constexpr int D = 128, HALF = 64;
+    constexpr int HALF = D / 2, LPH = D / 8, HPW = 256 / LPH;   // lanes, heads per work-group
     using V = Vec4<T>;
-    const int t = blockIdx.x, h = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
+    const int t = blockIdx.x, h = blockIdx.y * HPW + threadIdx.x / LPH, u = threadIdx.x % LPH;
     if (h >= H) return;   // a whole 16-lane group
     const size_t src = ((size_t)t * H + h) * D;
     float ka[4], kb[4], va[4], vb[4];
@@ -455,24 +457,24 @@ __global__ void __launch_bounds__(256) store_kv_int8_v_kernel(int8_t *__restrict
         y[e] = va[e];
         y[4 + e] = vb[e];
     }
-    quantize16(x, lq + (size_t)row * D, 4 * u, HALF + 4 * u, ls + row, u);
-    quantize16(y, lq + half_q + (size_t)row * D, 4 * u, HALF + 4 * u, ls + half_s + row, u);
+    quantize_group<LPH>(x, lq + (size_t)row * D, 4 * u, HALF + 4 * u, ls + row, u);
+    quantize_group<LPH>(y, lq + half_q + (size_t)row * D, 4 * u, HALF + 4 * u, ls + half_s + row, u);
 }
 
-// rope for head_dim 128 with the fused kernel's layout: 16 lanes per head (lane u holds
-// pair elements 4u .. 4u + 3 and 64 + 4u .. 64 + 4u + 3), 16 heads per 256-thread
-// work-group; the head's elements load before the position does. Same formula and rounding
+// rope for head_dim 128 or 64 with the fused kernel's layout: D / 8 lanes per head (lane u
+// holds pair elements 4u .. 4u + 3 and D/2 + 4u .. D/2 + 4u + 3), 2048 / D heads per
+// 256-thread work-group; the head's elements load before the position does. Same formula and rounding
 // as rope_kernel; rows at positions outside the table are left untouched.
-template <typename T>
+template <typename T, int D>
 __global__ void __launch_bounds__(256) rope_v_kernel(T *__restrict__ y, const T *__restrict__ x,
                                                      const T *__restrict__ cos_t,
                                                      const T *__restrict__ sin_t, int table_len,
                                                      const int32_t *__restrict__ positions,
                                                      int heads) {
-    constexpr int D = 128, HALF = 64;
+    constexpr int HALF = D / 2, LPH = D / 8, HPW = 256 / LPH;   // lanes, heads per work-group
     using E = Elt<T>;
     using V = Vec4<T>;
-    const int t = blockIdx.x, h = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
+    const int t = blockIdx.x, h = blockIdx.y * HPW + threadIdx.x / LPH, u = threadIdx.x % LPH;
     if (h >= heads) return;   // a whole 16-lane group
     const size_t base = ((size_t)t * heads + h) * D;
     float a[4], b[4];
@@ -495,17 +497,17 @@ __global__ void __launch_bounds__(256) rope_v_kernel(T *__restrict__ y, const T 
     V::st(y + base + HALF + 4 * u, y2);
 }
 
-// Dense store_kv for head_dim 128: 16 lanes per KV head, 16 heads per 256-thread
-// work-group, each lane moving its 16-byte chunks of the key and value rows (bit copies),
+// Dense store_kv for head_dim 128 or 64: D / 8 lanes per KV head, 2048 / D heads per
+// 256-thread work-group, each lane moving its 16-byte chunks of the key and value rows (bit copies),
 // loaded before the slot is.
-template <typename T>
+template <typename T, int D>
 __global__ void __launch_bounds__(256) store_kv_v_kernel(T *__restrict__ kp, T *__restrict__ vp,
                                                          const T *__restrict__ k,
                                                          const T *__restrict__ v,
                                                          const int32_t *__restrict__ slots, int P,
                                                          int H, int pages) {
-    constexpr int D = 128, CH = D * (int)sizeof(T) / 16 / 16;   // 16-byte chunks per lane
-    const int t = blockIdx.x, h = blockIdx.y * 16 + (threadIdx.x >> 4), u = threadIdx.x & 15;
+    constexpr int LPH = D / 8, HPW = 256 / LPH, CH = D * (int)sizeof(T) / 16 / LPH;   // 16-byte chunks per lane
+    const int t = blockIdx.x, h = blockIdx.y * HPW + threadIdx.x / LPH, u = threadIdx.x % LPH;
     if (h >= H) return;   // a whole 16-lane group
     const size_t src = ((size_t)t * H + h) * D;
     const uint4 *ks = reinterpret_cast<const uint4 *>(k + src);
@@ -513,8 +515,8 @@ __global__ void __launch_bounds__(256) store_kv_v_kernel(T *__restrict__ kp, T *
     uint4 kc[CH], vc[CH];
 #pragma unroll
     for (int c = 0; c < CH; c++) {
-        kc[c] = ks[u + 16 * c];
-        vc[c] = vs[u + 16 * c];
+        kc[c] = ks[u + LPH * c];
+        vc[c] = vs[u + LPH * c];
     }
     const long long row = slot_row(slots[t], h, P, H, pages);
     if (row < 0) return;   // the whole group
@@ -522,8 +524,8 @@ __global__ void __launch_bounds__(256) store_kv_v_kernel(T *__restrict__ kp, T *
     uint4 *vd = reinterpret_cast<uint4 *>(vp + (size_t)row * D);
 #pragma unroll
     for (int c = 0; c < CH; c++) {
-        kd[u + 16 * c] = kc[c];
-        vd[u + 16 * c] = vc[c];
+        kd[u + LPH * c] = kc[c];
+        vd[u + LPH * c] = vc[c];
     }
 }
 
@@ -541,15 +543,21 @@ int ti_launch_rmsnorm(int dtype, void *y, const void *x, const void *w, int rows
 int ti_launch_rope(int dtype, void *y, const void *x, const void *cos_t, const void *sin_t,
                    int table_len, const int32_t *positions, int n, int heads, int D,
                    hipStream_t s) {
-    if (D == 128) {
-        const dim3 vgrid(n, (heads + 15) / 16);
-        if (dtype == TI_BF16)
-            rope_v_kernel<uint16_t><<<vgrid, 256, 0, s>>>((uint16_t *)y, (const uint16_t *)x,
-                                                          (const uint16_t *)cos_t, (const uint16_t *)sin_t,
-                                                          table_len, positions, heads);
-        else
-            rope_v_kernel<float><<<vgrid, 256, 0, s>>>((float *)y, (const float *)x, (const float *)cos_t,
-                                                       (const float *)sin_t, table_len, positions, heads);
+    if (D == 128 || D == 64) {
+        const int hpw = 2048 / D;   // heads per 256-thread work-group (D / 8 lanes per head)
+        const dim3 vgrid(n, (heads + hpw - 1) / hpw);
+#define TI_ROPE_V(DD)                                                                              \
+    if (dtype == TI_BF16)                                                                          \
+        rope_v_kernel<uint16_t, DD><<<vgrid, 256, 0, s>>>((uint16_t *)y, (const uint16_t *)x,       \
+                                                          (const uint16_t *)cos_t,                  \
+                                                          (const uint16_t *)sin_t, table_len,       \
+                                                          positions, heads);                        \
+    else                                                                                           \
+        rope_v_kernel<float, DD><<<vgrid, 256, 0, s>>>((float *)y, (const float *)x,                \
+                                                       (const float *)cos_t, (const float *)sin_t,  \
+                                                       table_len, positions, heads);
+        if (D == 128) { TI_ROPE_V(128) } else { TI_ROPE_V(64) }
+#undef TI_ROPE_V
         return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
     }
     dim3 grid(n, (heads * (D / 2) + 255) / 256);
@@ -567,26 +575,31 @@ int ti_launch_store_kv(int dtype, const ti_kv_cache *c, const void *k, const voi
                        const int32_t *slots, int n, hipStream_t s) {
     dim3 grid(n, c->kv_heads);
     const int D = c->head_dim, P = c->page_size, H = c->kv_heads, pages = c->num_pages;
-    if (c->kind == TI_KV_INT8 && D == 128) {
-        const dim3 vgrid(n, (H + 15) / 16);
-        if (dtype == TI_BF16)
-            store_kv_int8_v_kernel<uint16_t><<<vgrid, 256, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
-                                                                   (const uint16_t *)k, (const uint16_t *)v,
-                                                                   slots, P, H, pages);
-        else
-            store_kv_int8_v_kernel<float><<<vgrid, 256, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
-                                                                (const float *)k, (const float *)v, slots,
-                                                                P, H, pages);
-    } else if (c->kind != TI_KV_INT8 && D == 128) {
-        const dim3 vgrid(n, (H + 15) / 16);
-        if (dtype == TI_BF16)
-            store_kv_v_kernel<uint16_t><<<vgrid, 256, 0, s>>>((uint16_t *)c->k_pages, (uint16_t *)c->v_pages,
-                                                              (const uint16_t *)k, (const uint16_t *)v, slots,
-                                                              P, H, pages);
-        else
-            store_kv_v_kernel<float><<<vgrid, 256, 0, s>>>((float *)c->k_pages, (float *)c->v_pages,
-                                                           (const float *)k, (const float *)v, slots, P, H,
-                                                           pages);
+    const int hpw = 2048 / D;   // heads per 256-thread work-group (D / 8 lanes per head)
+    const dim3 vgrid(n, (H + hpw - 1) / hpw);
+#define TI_STORE_V(DD)                                                                             \
+    if (c->kind == TI_KV_INT8) {                                                                   \
+        if (dtype == TI_BF16)                                                                      \
+            store_kv_int8_v_kernel<uint16_t, DD><<<vgrid, 256, 0, s>>>(                            \
+                c->layer_q, c->layer_scale, c->smooth, (const uint16_t *)k, (const uint16_t *)v,    \
+                slots, P, H, pages);                                                                \
+        else                                                                                       \
+            store_kv_int8_v_kernel<float, DD><<<vgrid, 256, 0, s>>>(                               \
+                c->layer_q, c->layer_scale, c->smooth, (const float *)k, (const float *)v, slots,  \
+                P, H, pages);                                                                       \
+    } else if (dtype == TI_BF16) {                                                                 \
+        store_kv_v_kernel<uint16_t, DD><<<vgrid, 256, 0, s>>>(                                     \
+            (uint16_t *)c->k_pages, (uint16_t *)c->v_pages, (const uint16_t *)k,                    \
+            (const uint16_t *)v, slots, P, H, pages);                                               \
+    } else {                                                                                       \
+        store_kv_v_kernel<float, DD><<<vgrid, 256, 0, s>>>((float *)c->k_pages, (float *)c->v_pages, \
+                                                           (const float *)k, (const float *)v,      \
+                                                           slots, P, H, pages);                     \
+    }
+    if (D == 128) {
+        TI_STORE_V(128)
+    } else if (D == 64) {
+        TI_STORE_V(64)
     } else if (c->kind == TI_KV_INT8) {
         if (dtype == TI_BF16)
             store_kv_int8_kernel<uint16_t><<<grid, 64, 0, s>>>(c->layer_q, c->layer_scale, c->smooth,
@@ -605,6 +618,7 @@ int ti_launch_store_kv(int dtype, const ti_kv_cache *c, const void *k, const voi
                                                    (const float *)k, (const float *)v, slots, D, P,
                                                    H, pages);
     }
+#undef TI_STORE_V
     return hipGetLastError() == hipSuccess ? TI_OK : TI_ERR_LAUNCH;
 }
 
@@ -613,12 +627,16 @@ static void launch_inputs(void *q_out, const ti_kv_cache *c, const void *qkv, co
                           const void *k_norm, const void *cos_sin, int table_len,
                           const int32_t *positions, const int32_t *slots, int n, int nq,
                           float eps, hipStream_t s) {
-    if (c->head_dim == 128) {
-        dim3 grid(n, (nq + c->kv_heads + 15) / 16);
-        attention_inputs_v_kernel<T, NORM, INT8><<<grid, 256, 0, s>>>(
-            (T *)q_out, (T *)c->k_pages, (T *)c->v_pages, c->layer_q, c->layer_scale, c->smooth,
-            (const T *)qkv, (const T *)q_norm, (const T *)k_norm, (const T *)cos_sin, table_len,
-            positions, slots, nq, c->kv_heads, c->page_size, c->num_pages, eps);
+    if (c->head_dim == 128 || c->head_dim == 64) {
+        const int hpw = 2048 / c->head_dim;   // heads per 256-thread work-group
+        dim3 grid(n, (nq + c->kv_heads + hpw - 1) / hpw);
+#define TI_INPUTS_V(DD)                                                                            \
+    attention_inputs_v_kernel<T, NORM, INT8, DD><<<grid, 256, 0, s>>>(                             \
+        (T *)q_out, (T *)c->k_pages, (T *)c->v_pages, c->layer_q, c->layer_scale, c->smooth,        \
+        (const T *)qkv, (const T *)q_norm, (const T *)k_norm, (const T *)cos_sin, table_len,        \
+        positions, slots, nq, c->kv_heads, c->page_size, c->num_pages, eps);
+        if (c->head_dim == 128) { TI_INPUTS_V(128) } else { TI_INPUTS_V(64) }
+#undef TI_INPUTS_V
         return;
     }
     dim3 grid(n, nq + c->kv_heads);
