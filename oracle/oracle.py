@@ -21,8 +21,8 @@ _lib = None
 
 
 def build() -> str:
-    """Compile liboracle.so with the committed Makefile (gcc, OpenMP)."""
-    subprocess.run(["make", "-s", "-C", _HERE, "liboracle.so"], check=True)
+    """Compile liboracle.so with the committed Makefile (gcc, OpenMP), every time (-B)."""
+    subprocess.run(["make", "-s", "-B", "-C", _HERE, "liboracle.so"], check=True)
     return _LIB
 
 
