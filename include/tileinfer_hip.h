@@ -154,12 +154,16 @@ int ti_attention(const ti_attention_args *args, const ti_kv_cache *cache, void *
  * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc). It calls no hipMalloc / hipFree and no allocating library routine.
  * Same arguments, kernels and results as ti_attention with a sufficient workspace;
- * args->workspace and args->workspace_bytes are ignored. Shapes whose workspace
- * (ti_attention_workspace_bytes) exceeds the scratch are rejected with TI_ERR_WORKSPACE
- * before anything is launched. Every call on one GPU shares that GPU's scratch: calls that
- * overlap on one GPU (several streams, several host threads) race and must be serialized
- * by the caller. Nothing in the scratch needs clearing between calls (every partial a
- * launch reads is written by the same launch). `stream` must belong to the current device.
+ * args->workspace and args->workspace_bytes are ignored. Where the workspace
+ * (ti_attention_workspace_bytes) exceeds the scratch, prefill and fp32 steps run unsplit
+ * (as ti_attention does without a workspace) and decode steps, whose workspace is
+ * mandatory, are rejected with TI_ERR_WORKSPACE before anything is launched. Every call on
+ * one GPU shares that GPU's scratch: calls that overlap on one GPU (several streams,
+ * several host threads) race and must be serialized by the caller. Nothing in the scratch
+ * needs clearing between calls (every partial a launch reads is written by the same
+ * launch). `stream` must belong to the current device (TI_ERR_INVALID_ARG otherwise).
+ * The scratch is reserved on every GPU where the library's code object is loaded, whether
+ * or not this entry point is called.
  */
 int ti_attention_noalloc(const ti_attention_args *args, const ti_kv_cache *cache, void *stream);
 

@@ -148,6 +148,20 @@ def test_unsupported_shapes_and_workspace():
     assert ws(a, c)[0] == _lib.TI_OK
 
 
+def test_paired_prefill_grid_counts_pairs():
+    """A paired prefill holds two q-tiles per work-group: its grid y is (q-tiles + 1) / 2,
+    so a pinned 16-row paired step of 65536-131070 q-tiles (G = 32: one position per
+    q-tile) fits the grid, and one of 131072 does not."""
+    L = ti.load_library()
+    c = _cache(kv_heads=1, num_pages=10000)
+    for n, want in ((100000, _lib.TI_OK), (131070, _lib.TI_OK), (131072, _lib.TI_ERR_UNSUPPORTED)):
+        a = _args(q_heads=32, num_seqs=1, max_query_len=n, total_tokens=n, block_table_stride=8192,
+                  path=_lib.TI_PATH_PREFILL_PAIRED16)
+        assert ws(a, c)[0] == want, n
+        if want != _lib.TI_OK:
+            assert L.ti_attention(ctypes.byref(a), ctypes.byref(c), None) == want
+
+
 def test_store_rope_inputs_validation():
     L = ti.load_library()
     c = _cache()
@@ -188,7 +202,8 @@ def test_noalloc_validates_before_any_hip_call():
               path=_lib.TI_PATH_PREFILL_PINGPONG)
     st, need = ws(a, c)
     assert st == _lib.TI_OK and need > _lib.NOALLOC_SCRATCH_BYTES
-    assert L.ti_attention_noalloc(ctypes.byref(a), ctypes.byref(c), None) == _lib.TI_ERR_WORKSPACE
+    # (such a prefill runs unsplit through ti_attention_noalloc, as ti_attention does without
+    # a workspace: tests/test_zz_no_alloc.py runs it on the GPU)
     # 256 tokens: half the rows, within the scratch (not launched here: no GPU)
     a = _args(q_heads=8, num_seqs=1, max_query_len=256, total_tokens=256,
               path=_lib.TI_PATH_PREFILL_PINGPONG)

@@ -208,22 +208,29 @@ def test_out_of_range_slots_are_skipped(gpu):
     assert kp[0, :, 1].float().eq(1).all()
 
 
+@pytest.mark.parametrize("int8", [False, True], ids=["dense", "int8"])
 @pytest.mark.parametrize("D", [64, 128])
-def test_attention_inputs_out_of_range(gpu, D):
+def test_attention_inputs_out_of_range(gpu, D, int8):
     """Tokens whose slot lies outside the pool write no K/V row, tokens whose position
     lies outside the rotary table write nothing (the q rows keep what they held); every
-    other token is written as the oracle writes it. D = 128 runs the 16-lanes-per-head
-    kernel, D = 64 the one-wave-per-head kernel."""
+    other token is written as the oracle writes it. Both head dims run the D / 8 lanes per
+    head kernel; on INT8 pages the untouched rows and scales keep their prior contents."""
     nq, nkv, P, pages, L = 4, 2, 4, 3, 32
-    g = rng(700 + D)
+    g = rng(700 + D + (1 if int8 else 0))
     positions = np.array([3, 5, 40, 7], np.int32)            # 40 is past the table
     slots = np.array([2, 13, 5, 0], np.int32)                # 13 and 0 are outside the pool
     n = len(positions)
     c, s, table = _table(g, D, L, True)
     qkv = randn(g, n, nq + 2 * nkv, D, bf16=True)
     q = torch.full((n, nq, D), 7.0, dtype=torch.bfloat16, device="cuda")
-    kp = torch.zeros((pages, nkv, P, D), dtype=torch.bfloat16, device="cuda")
-    vp = torch.zeros_like(kp)
+    if int8:
+        cs = (g.random(D, dtype=np.float32) + 0.5).astype(np.float32)
+        kp, vp = ti.int8_kv_pools(D, P, nkv, pages, key_smoothing=torch.from_numpy(cs))
+        kp.layer_q.fill_(55)                                 # prior contents
+        kp.layer_scale.fill_(0.25)
+    else:
+        kp = torch.zeros((pages, nkv, P, D), dtype=torch.bfloat16, device="cuda")
+        vp = torch.zeros_like(kp)
     ti.attention_inputs_(BE, q, kp, vp, dev(qkv, True), None, None, table,
                          torch.from_numpy(positions).cuda(), torch.from_numpy(slots).cuda(), 1e-6)
     keep = np.array([0, 1, 3])                               # tokens with an in-table position
@@ -231,11 +238,20 @@ def test_attention_inputs_out_of_range(gpu, D):
     scratch = [np.zeros((pages, nkv, P, D), np.float32) for _ in range(2)]
     rq = orc.attention_inputs(qkv[keep], None, None, cs_tab, positions[keep], np.ones(3, np.int32),
                               nq, nkv, 1e-6, True, k_pages=scratch[0], v_pages=scratch[1])
-    # only token 0 has both an in-table position and an in-pool slot
-    rkp, rvp = np.zeros((pages, nkv, P, D), np.float32), np.zeros((pages, nkv, P, D), np.float32)
-    orc.attention_inputs(qkv[:1], None, None, cs_tab, positions[:1], slots[:1], nq, nkv, 1e-6, True,
-                         k_pages=rkp, v_pages=rvp)
     got_q = host(q)
     assert np.array_equal(got_q[keep], rq)
     assert (got_q[2] == 7.0).all()
-    assert np.array_equal(host(kp), rkp) and np.array_equal(host(vp), rvp)
+    # only token 0 has both an in-table position and an in-pool slot
+    if int8:
+        rlq = np.full((2, pages, nkv, P, D), 55, np.int8)
+        rls = np.full((2, pages, nkv, P), 0.25, np.float32)
+        orc.attention_inputs(qkv[:1], None, None, cs_tab, positions[:1], slots[:1], nq, nkv, 1e-6, True,
+                             layer_q=rlq, layer_scale=rls, smooth=cs)
+        assert np.array_equal(kp.layer_q.cpu().numpy(), rlq)
+        assert np.array_equal(kp.layer_scale.cpu().numpy(), rls)
+        assert (rlq != 55).any()                             # the in-range token was written
+    else:
+        rkp, rvp = np.zeros((pages, nkv, P, D), np.float32), np.zeros((pages, nkv, P, D), np.float32)
+        orc.attention_inputs(qkv[:1], None, None, cs_tab, positions[:1], slots[:1], nq, nkv, 1e-6, True,
+                             k_pages=rkp, v_pages=rvp)
+        assert np.array_equal(host(kp), rkp) and np.array_equal(host(vp), rvp)

@@ -35,6 +35,10 @@ CASES = [
     ("decode_flat", "bf16", 32, 8, 16, [(6, 3000, 1), (4, 700, 1)], _lib.TI_PATH_AUTO),
     ("prefill_paired16", "bf16", 32, 8, 16, [(1, 0, 512), (1, 1024, 128)], _lib.TI_PATH_AUTO),
     ("prefill_paired16_int8", "int8", 32, 8, 16, [(1, 0, 512), (1, 300, 200)], _lib.TI_PATH_AUTO),
+    # the ping-pong kernel pinned on 512 tokens of one KV head with G = 8: its split partials
+    # (16 x 4096 rows) exceed the scratch, so noalloc runs it unsplit, as ti_attention does
+    # without a workspace; the second call fits the scratch and splits
+    ("prefill_pp_over_scratch", "bf16", 8, 1, 16, [(1, 0, 512), (1, 0, 256)], _lib.TI_PATH_PREFILL_PINGPONG),
 ]
 
 
@@ -82,6 +86,8 @@ def test_noalloc_matches_attention(gpu, case):
         print(f"noalloc {name} call {i}: B={B} start={start} n={n} path={path}", flush=True)
         x = _inputs(g, kind, Hq, Hk, P, B, start, n)
         ws = ti.attention_workspace(BE, x["qd"], x["k"], num_seqs=B, max_query_len=n, path=path)
+        if ws is not None and ws.numel() > _lib.NOALLOC_SCRATCH_BYTES:
+            ws = None                               # noalloc runs this shape unsplit
         want = _call("ti_attention", x, path, ws)
         got = _call("ti_attention_noalloc", x, path, None)
         torch.cuda.synchronize()
@@ -95,3 +101,36 @@ def test_noalloc_matches_attention(gpu, case):
                                 **x["ref_kw"])
             err = float(np.max(np.abs(ref - got_h[b * n:(b + 1) * n])))
             assert err <= tol, f"call {i} seq {b}: max abs err {err}"
+
+
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[8]], ids=lambda c: c[0])
+def test_noalloc_allocates_nothing_and_replays_in_a_graph(gpu, case):
+    """The defining property: no allocation. The eager call leaves torch's allocator
+    untouched, and the call captured in a HIP graph replays (several times, with eager work
+    and synchronizations between the replays) to the eager output bit for bit."""
+    name, kind, Hq, Hk, P, calls, path = case
+    g = rng(5300 + len(name))
+    B, start, n = calls[0]
+    print(f"noalloc graph {name}: B={B} start={start} n={n}", flush=True)
+    x = _inputs(g, kind, Hq, Hk, P, B, start, n)
+    out = torch.full_like(x["qd"], float("nan"))
+    a = _attention_args(out, x["qd"], x["btd"], x["pos"], 1 / math.sqrt(128), True, path, B, n, None, None)
+    c = kv_cache_struct(x["k"], x["v"])
+    L = _lib.load()
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    assert L.ti_attention_noalloc(ctypes.byref(a), ctypes.byref(c), _stream(x["qd"])) == _lib.TI_OK
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == before
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = L.ti_attention_noalloc(ctypes.byref(a), ctypes.byref(c), _stream(x["qd"]))
+    assert st == _lib.TI_OK
+    for r in range(4):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r} differs from the eager call"
+        x["qd"].mul_(1.0)                           # eager work between replays
+        torch.cuda.synchronize()

@@ -88,6 +88,12 @@ int check_attention(const ti_attention_args *a, const ti_kv_cache *c) {
     return TI_OK;
 }
 
+// Grid y of a prefill launch: paired plans hold two q-tiles per work-group, the others one
+// q-tile per key split. At most 65535.
+long long prefill_grid_y(const ti_prefill_plan &pl) {
+    return pl.pair ? (pl.qtiles + 1LL) / 2 : (long long)pl.qtiles * pl.splits;
+}
+
 }  // namespace
 
 extern "C" {
@@ -115,9 +121,10 @@ int ti_attention_workspace_bytes(const ti_attention_args *a, const ti_kv_cache *
     if (path == 0) ti_plan_generic(a, c, bytes);
     if (path == 1) *bytes = ti_plan_decode(a, c).bytes;
     if (path == 2) {
-        const ti_prefill_plan pp = ti_plan_prefill(a, c, false);
-        if (pp.qtiles > 65535) return TI_ERR_UNSUPPORTED;
-        *bytes = (long long)pp.qtiles * pp.splits > 65535 ? 0 : pp.bytes;
+        ti_prefill_plan pp = ti_plan_prefill(a, c, false);
+        if (prefill_grid_y(pp) > 65535) pp.splits = 1, pp.bytes = 0;   // runs unsplit
+        if (prefill_grid_y(pp) > 65535) return TI_ERR_UNSUPPORTED;
+        *bytes = pp.bytes;
     }
     return TI_OK;
 }
@@ -133,8 +140,8 @@ int ti_attention(const ti_attention_args *a, const ti_kv_cache *c, void *stream)
         // The prefill path never requires a workspace (the reference runs its prefill
         // kernel exactly when none is passed); without one it runs unsplit.
         ti_prefill_plan pp = ti_plan_prefill(a, c, true);
-        if ((long long)pp.qtiles * pp.splits > 65535) pp.splits = 1;
-        if (pp.qtiles > 65535) return TI_ERR_UNSUPPORTED;   // q-tiles share grid y (at most 65535)
+        if (prefill_grid_y(pp) > 65535) pp.splits = 1, pp.bytes = 0;
+        if (prefill_grid_y(pp) > 65535) return TI_ERR_UNSUPPORTED;   // q-tiles share grid y
         if (pp.bytes > 0 && (!a->workspace || a->workspace_bytes < pp.bytes)) {
             pp.splits = 1;
             pp.bytes = 0;
@@ -147,13 +154,25 @@ int ti_attention(const ti_attention_args *a, const ti_kv_cache *c, void *stream)
 }
 
 int ti_attention_noalloc(const ti_attention_args *a, const ti_kv_cache *c, void *stream) {
-    // The same validation and the same plan as ti_attention; the plan's workspace (sized
-    // as ti_attention_workspace_bytes, which bounds every launch of these shapes) must fit
-    // the static scratch, else the call is rejected before any HIP call.
+    // The same validation and the same plan as ti_attention. The plan's workspace (sized
+    // as ti_attention_workspace_bytes, which bounds every launch of these shapes) comes from
+    // the static scratch when it fits. Prefill and fp32 steps whose split partials would not
+    // fit run unsplit, as ti_attention does without a workspace; a decode step, whose
+    // workspace is mandatory, is rejected before any HIP call.
     size_t need = 0;
     int st = ti_attention_workspace_bytes(a, c, &need);
     if (st) return st;
-    if (need > (size_t)TI_NOALLOC_SCRATCH_BYTES) return TI_ERR_WORKSPACE;
+    if (need > (size_t)TI_NOALLOC_SCRATCH_BYTES) {
+        if (resolve_path(a, c) == 1) return TI_ERR_WORKSPACE;
+        need = 0;
+    }
+    // The scratch address is per GPU: the stream must belong to the current GPU.
+    if (stream) {
+        int sdev = -1, dev = -1;
+        if (hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess || hipGetDevice(&dev) != hipSuccess)
+            return TI_ERR_INVALID_ARG;
+        if (sdev != dev) return TI_ERR_INVALID_ARG;
+    }
     ti_attention_args local = *a;
     local.workspace = nullptr;
     local.workspace_bytes = 0;

@@ -132,29 +132,13 @@ ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c) 
     const int G = a->q_heads / c->kv_heads;
     pl.rows = G * a->max_query_len;
     const long long pairs = (long long)a->num_seqs * c->kv_heads;
-    // TI_DECODE_TARGET_WGS / TI_DECODE_MAX_SPLITS / TI_DECODE_SPLITS / TI_DECODE_WAVES
-    // override the defaults (tuning only).
     // Split target: 256 work-groups of 4 waves, one wave per SIMD (B = 8: 4 splits against
     // 8, same box: INT8 x 32768 101.6 vs 102.9 us, bf16 x 4096 29.4 vs 30.0 us).
-    static const long long target = [] {
-        const char *e = getenv("TI_DECODE_TARGET_WGS");
-        return e ? atoll(e) : 256LL;
-    }();
+    constexpr long long target = 256;
     // At most 16 splits: at B = 1 (8 KV heads) 16 splits beat 32 at every context
     // measured (1024 positions 7.7 vs 8.8 us, 2048 8.6 vs 9.9, 4096 11.0 vs 11.5): fewer
     // idle waves on short contexts and half the partials to merge.
-    static const int max_splits = [] {
-        const char *e = getenv("TI_DECODE_MAX_SPLITS");
-        return e ? atoi(e) : 16;
-    }();
-    static const int forced = [] {
-        const char *e = getenv("TI_DECODE_SPLITS");
-        return e ? atoi(e) : 0;
-    }();
-    static const int forced_waves = [] {
-        const char *e = getenv("TI_DECODE_WAVES");
-        return e ? atoi(e) : 0;
-    }();
+    constexpr int max_splits = 16;
     // Batches of at least 256 (sequence, KV head) pairs: one split of 4 waves per pair, one
     // wave per SIMD (measured against 8 waves, same process: B = 32 x 4096 91.1 vs 91.8 us,
     // ragged B = 32 132.0 vs 133.9 us; two tiles per step or three register sets in flight
@@ -163,20 +147,14 @@ ti_decode_plan ti_plan_decode(const ti_attention_args *a, const ti_kv_cache *c) 
     if (pairs < 256 || pl.rows > 32) {
         while (sp < max_splits && pairs * sp < target) sp <<= 1;
     }
-    if (forced > 0) sp = forced;
-    if ((forced_waves == 4 || forced_waves == 8) && pl.rows <= 32) nw = forced_waves;
     // Split batches of 4-64 sequences with at least 4 splits each share their work-groups out
     // by length (flat mode): the same B x splits work-groups per KV head, cut in proportion
-    // to each sequence's keys (TI_DECODE_FLAT=0 turns it off, tuning only). Measured on
+    // to each sequence's keys. Measured on
     // lengths drawn from [1024, 8192] against the fixed splits (separate processes, same
     // box): B = 8 (4 splits) 31.0 -> 27.5 us, B = 4 (8 splits) 21.3 vs 21.3 us, but B = 2
     // (16 splits) 16.0 -> 16.9 us and B = 16 (2 splits) 60.8 -> 63.0 us, where the shares
     // balance little and the device-side prefix costs its latency.
-    static const int flat_on = [] {
-        const char *e = getenv("TI_DECODE_FLAT");
-        return e ? atoi(e) : 1;
-    }();
-    pl.flat = flat_on && sp >= 4 && a->num_seqs >= 4 && a->num_seqs <= 64 ? sp * a->num_seqs : 0;
+    pl.flat = sp >= 4 && a->num_seqs >= 4 && a->num_seqs <= 64 ? sp * a->num_seqs : 0;
     pl.splits = sp;
     pl.waves = nw;
     pl.bytes = sp == 1 ? 0 : (size_t)pairs * sp * pl.rows * (c->head_dim + 2) * sizeof(float);

@@ -719,14 +719,15 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         }
 }
 
-// One 16-byte-per-lane direct global -> LDS load issued from inline assembly (scalar base,
-// per-lane 32-bit byte offset; NT: cache-policy bits sc0 nt). The compiler does not see
-// its LDS write, so it adds no waits of its own before LDS reads of the other buffer; the
-// caller waits with an explicit vmcnt and a barrier before any wave reads the tile.
-// lds_addr is wave-uniform (it goes to M0). M0 cannot be declared clobbered (the compiler
-// reserves it); the kernel that uses these helpers has no other use of M0 (gfx9 LDS
-// instructions need no M0 set-up, and it indexes no register arrays dynamically; its gfx950
-// assembly has no M0 write besides these statements).
+// One 16-byte-per-lane direct global -> LDS load (global_load_lds_dwordx4 through the
+// compiler's builtin, which sets M0 itself), from a wave-uniform base plus a per-lane byte
+// offset (NT: cache-policy bits 3, sc0 nt). The LDS address must be wave-uniform. The caller
+// waits with an explicit vmcnt and a barrier before any wave reads the tile; the compiler
+// adds a vmcnt(0) of its own before the transposing V reads that follow a step's loads
+// (it cannot tell the two buffers apart), which costs 0.1-1.0 us per call against issuing
+// the same loads from inline assembly (measured: 512 tokens 9.99 -> 10.27 us, chunked 512 on
+// 1024 19.07 -> 19.82, 1024 tokens 23.6 -> 24.6), the price of leaving M0 to the compiler.
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
 template <bool NT>
 __device__ __forceinline__ void lds_dma16(const void *base, uint32_t voff, uint32_t lds) {
     // the base and the LDS address are wave-uniform: pin them in scalar registers
@@ -734,23 +735,15 @@ __device__ __forceinline__ void lds_dma16(const void *base, uint32_t voff, uint3
     // (readfirstlane returns int: each half goes through uint32_t, never sign-extended)
     const uint64_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
     const uint64_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
-    const void *sbase = reinterpret_cast<const void *>((hi << 32) | lo);
+    const char *sbase = reinterpret_cast<const char *>((hi << 32) | lo);
     const uint32_t lds_addr = (uint32_t)__builtin_amdgcn_readfirstlane(lds);
-    if (NT)
-        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc0 nt" ::"v"(voff), "s"(sbase), "s"(lds_addr)
-                     : "memory");
-    else
-        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_addr)
-                     : "memory");
+    __builtin_amdgcn_global_load_lds(sbase + voff, (lds_ptr_t)(size_t)lds_addr, 16, 0, NT ? 3 : 0);
 }
 // The same from a per-lane 64-bit address (the step's last tile, whose rows are clamped per key).
 template <bool NT>
 __device__ __forceinline__ void lds_dma16_v(const void *gptr, uint32_t lds) {
     const uint32_t lds_addr = (uint32_t)__builtin_amdgcn_readfirstlane(lds);
-    if (NT)
-        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off sc0 nt" ::"v"(gptr), "s"(lds_addr) : "memory");
-    else
-        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_addr) : "memory");
+    __builtin_amdgcn_global_load_lds(gptr, (lds_ptr_t)(size_t)lds_addr, 16, 0, NT ? 3 : 0);
 }
 
 // Paired q-tiles on 16-row waves (bf16 activations, D = 128, pages of 2^k >= 16 tokens,
@@ -770,8 +763,8 @@ __device__ __forceinline__ void lds_dma16_v(const void *gptr, uint32_t lds) {
 //   O^T += V^T P^T  D/16 v_mfma_f32_16x16x32_bf16; B = P^T is the score registers (k-index
 //                   8 kg + j: key 4 kg + j, then 16 + 4 kg + j - 4), A = V^T from two 8-B
 //                   transposing reads (rows 4 kg .. + 3 and 16 + 4 kg .. + 3).
-// A step issues the next tile's loads first (dense: direct loads into the other buffer,
-// from inline assembly; INT8: loads into registers, converted to bf16 and stored into the
+// A step issues the next tile's loads first (dense: direct loads into the other buffer;
+// INT8: loads into registers, converted to bf16 and stored into the
 // other buffer after the step's compute), then reads this tile's keys, runs the score MFMAs
 // and the softmax, and only then reads the values, so key and value operands never occupy
 // registers together. The pair's 64 query rows come through LDS (one direct load per lane),
@@ -1162,20 +1155,7 @@ void launch_prefill_d(const PrefillParams &p, int wpg, int ng, bool dl, dim3 gri
 // per work-group, and key splits across work-groups, chosen so small prefills and verify
 // steps still spread over the 256 CUs. Depends only on host shapes (the block-table
 // width bounds the keys), never on positions, so a captured graph stays valid.
-// TI_PREFILL_WPG / TI_PREFILL_GROUPS / TI_PREFILL_SPLITS override (tuning only).
 ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c, bool bound_keys) {
-    static const int forced_wpg = [] {
-        const char *e = getenv("TI_PREFILL_WPG");
-        return e ? atoi(e) : 0;
-    }();
-    static const int forced_ng = [] {
-        const char *e = getenv("TI_PREFILL_GROUPS");
-        return e ? atoi(e) : 0;
-    }();
-    static const int forced_splits = [] {
-        const char *e = getenv("TI_PREFILL_SPLITS");
-        return e ? atoi(e) : 0;
-    }();
     ti_prefill_plan pl;
     const int G = a->q_heads / c->kv_heads;
     const long long pairs = (long long)c->kv_heads * a->num_seqs;
@@ -1194,7 +1174,7 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     pl.pair = 0;
     pl.r16 = 0;
     if (pl.pp) {
-        // Key splits (forced runs on small grids) while work-groups are fewer than the
+        // Key splits (pinned runs on small grids) while work-groups are fewer than the
         // CUs and every split keeps at least 8 key tiles of the longest context the
         // block tables can hold.
         pl.wpg = 8;
@@ -1205,19 +1185,16 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
         pl.splits = 1;
         while (pl.splits < 16 && wgs * pl.splits < 256 && (!bound_keys || key_tiles / (2 * pl.splits) >= 8))
             pl.splits *= 2;
-        if (forced_splits >= 1 && forced_splits <= 64) pl.splits = forced_splits;
         pl.rows = G * a->max_query_len;
         pl.bytes = pl.splits == 1 ? 0 : (size_t)pairs * pl.splits * pl.rows * (c->head_dim + 2) * sizeof(float);
         return pl;
     }
     pl.wpg = (long long)((a->max_query_len + 128 / G - 1) / (128 / G)) * pairs >= 256 ? 4 : 2;
-    if (forced_wpg == 2 || forced_wpg == 4) pl.wpg = forced_wpg;
     if (32 * pl.wpg < G) pl.wpg = 4;
     pl.TQ = 32 * pl.wpg / G;
     pl.qtiles = (a->max_query_len + pl.TQ - 1) / pl.TQ;
     const long long wgs = (long long)pl.qtiles * pairs;
     pl.ng = wgs >= 1024 ? 1 : (wgs >= 512 ? 2 : 4);
-    if (forced_ng == 1 || forced_ng == 2 || forced_ng == 4) pl.ng = forced_ng;
     if (pl.wpg == 4 && pl.ng > 2) pl.ng = 2;   // 16 waves of this kernel do not fit one CU's registers
     // Split the keys while work-groups are fewer than the CUs and every split keeps at
     // least 4 steps per key group of the longest context the block tables can hold.
@@ -1225,7 +1202,6 @@ ti_prefill_plan ti_plan_prefill(const ti_attention_args *a, const ti_kv_cache *c
     while (pl.splits < 16 && wgs * pl.splits < 256 &&
            (!bound_keys || key_tiles / (2 * pl.splits) >= 4LL * pl.ng))
         pl.splits *= 2;
-    if (forced_splits >= 1 && forced_splits <= 64) pl.splits = forced_splits;
     // Direct global -> LDS tile loads (bf16 dense cache, head_dim 128, pages of 2^k >= 16
     // tokens) for two-wave key groups, the small grids: measured 13.8 -> 12.4 us at a
     // 512-token prefill and 25.6 -> 23.3 us chunked, bit-identical; for four-wave groups

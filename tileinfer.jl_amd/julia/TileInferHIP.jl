@@ -6,7 +6,11 @@
 # C ABI's row-major layouts reversed, so every argument is passed as a pointer, no copy.
 #
 # Not exercised in this repository (no Julia toolchain in the build image); the Python
-# package tileinfer_hip drives the same entry points in the tests.
+# package tileinfer_hip drives the same entry points in the tests. It needs the reference's
+# allocations made array-generic first: the Int8Pages fields and int8_kv_pools
+# (src/ops/quant.jl:86-109), the cache pools (src/kv/paged_cache.jl:29), the rotary tables
+# (src/model/rope.jl:47) and StepBuffers (src/model/decoder.jl:72-112). The INT8 and
+# rotary methods below are typed on those generic types with ROCArray storage.
 module TileInferHIP
 
 using AMDGPU: ROCArray, ROCVector, stream
@@ -71,7 +75,7 @@ function kv_cache(k::ROCArray{T,4}, v::ROCArray{T,4}) where {T}
     KVCache(TI_KV_DENSE, D, P, H, pages, vptr(k), vptr(v), C_NULL, C_NULL, C_NULL)
 end
 
-function kv_cache(k::Int8Pages, v::Int8Pages)
+function kv_cache(k::Int8Pages{<:ROCArray}, v::Int8Pages{<:ROCArray})
     q, s, c = layer_arrays(k, v)                   # ArgumentError unless paired halves
     D, P, H, pages = size(k)
     KVCache(TI_KV_INT8, D, P, H, pages, C_NULL, C_NULL, pointer(q), pointer(s), pointer(c))
@@ -96,7 +100,7 @@ function workspace_query(q::ROCArray{T,3}) where {T}
 end
 
 # The shape-only ti_kv_cache of a pool (dense ROCArray or either Int8Pages half).
-function workspace_cache(k_pages)
+function workspace_cache(k_pages::Union{ROCArray,Int8Pages{<:ROCArray}})
     D, P, H, pages = size(k_pages)
     nz = Ptr{Cvoid}(1)
     k_pages isa Int8Pages ?
@@ -161,7 +165,7 @@ end
 
 # attention_inputs!(::TileBackend, ...): src/ops/tile/fused.jl:94-130
 function TileInfer.attention_inputs!(::HipBackend, q::ROCArray{T,3}, k_pages, v_pages, qkv,
-                                     q_norm, k_norm, table::RotaryTable, positions, slots,
+                                     q_norm, k_norm, table::RotaryTable{T,<:ROCArray}, positions, slots,
                                      eps::Real) where {T}
     D, nq, n = size(q)
     c = Ref(kv_cache(k_pages, v_pages))
