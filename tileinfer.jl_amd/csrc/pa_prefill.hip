@@ -139,9 +139,28 @@ struct Stage {
 
 // Page ids (0-based, clamped into the pool) of the two 16-key halves of tile kt, read with
 // scalar loads; fetched one tile ahead of use so their latency hides behind compute.
+// A wave-uniform int32 element as a scalar load (counted by lgkmcnt, never waiting on vector loads).
+__device__ __forceinline__ int sload(const int32_t *a, int idx) {
+    return ((const __attribute__((address_space(4))) int32_t *)a)[__builtin_amdgcn_readfirstlane(idx)];
+}
 struct TilePages {
     int pg[2];
 };
+
+// The block-table entries (1-based page ids, unclamped) of tile kt's two 16-key halves, as
+// scalar loads: their consumer clamps them (clamp_page), so the wait for these loads can sit
+// where the pages are used, a step later, instead of right after the loads.
+__device__ __forceinline__ TilePages raw_pages(const PrefillParams &p, const int32_t *bt, int kt) {
+    TilePages tp;
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+        const int idx = min((kt * KT + 16 * x) >> p.pshift, p.bt_stride - 1);   // PG16: P = 2^pshift; kt >= 0
+        tp.pg[x] = sload(bt, idx);
+    }
+    return tp;
+}
+// A raw block-table entry as a 0-based page inside the pool (as page_of_s).
+__device__ __forceinline__ int clamp_page(int raw, int num_pages) { return min(max(raw - 1, 0), num_pages - 1); }
 
 __device__ __forceinline__ TilePages tile_pages(const PrefillParams &p, const int32_t *bt, int kt) {
     TilePages tp;
@@ -794,12 +813,20 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     const int qt = p.qtiles - 1 - (int)blockIdx.y, qt_light = blockIdx.y;
     const int qtw = light ? qt_light : qt;
     const int b = blockIdx.z;
-    const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;
+    // the pointer arguments the prologue dereferences, loaded in the kernel arguments' first
+    // batch of scalar loads (left to itself the compiler loads some only after the query
+    // counts, a second dependent round trip before the first tile's loads)
+    asm volatile("" ::"s"(p.q), "s"(p.kp), "s"(p.vp), "s"(p.bt), "s"(p.positions), "s"(p.qsl));
+    const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
+    // The first tile's page ids do not depend on the step's positions: their scalar loads go
+    // out first, in the same batch as the query-count and position loads.
+    const TilePages spec = raw_pages(p, bt, grp);
+    const int tok0 = p.qsl ? sload(p.qsl, b) : b * p.nmax;
+    const int nb = p.qsl ? min(sload(p.qsl, b + 1) - tok0, p.nmax) : p.nmax;
+    const int start = max(sload(p.positions, tok0), 0), len = start + nb;
     const int t_first = qt * p.TQ;
     if (qt_light * p.TQ >= nb) return;
     const int t_first_w = qtw * p.TQ;
-    const int32_t *bt = p.bt + (size_t)b * p.bt_stride;
     // This lane's row: row rr of its q-tile (B operand of S^T: elements 32 i + 8 kg .. + 8).
     const int rr = 16 * (wl & 1) + r16, tl = rr / p.G, t = t_first_w + tl;
     const bool row_ok = tl < p.TQ && t < nb && !(light && qt_light == qt);
@@ -813,9 +840,41 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
         const uint16_t *src = p.q + ((size_t)(tok0 + (ok ? tq : 0)) * p.Hq + h * p.G + gq) * D + (qslot ^ (qrow & 15)) * 8;
         lds_dma16_v<false>(src, (uint32_t)(uintptr_t)(smem_raw + QOFF) + w * 1024);
     }
+    Bufs &dsm = reinterpret_cast<Bufs *>(smem_raw)[grp];
+    // direct loads: wave wl issues instructions q0, q0 + 1 of page half dx (instruction q4
+    // writes keys 4 q4 + lane / 16 of the half, 16-B slot lane % 16)
+    const int dx = wl / HW, q0 = NQ * (wl % HW);
+    const int ksub = lane >> 4, slot = lane & 15;
+    uint32_t koff[NQ], voff[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; u++) {
+        const int key = 4 * (q0 + u) + ksub;
+        koff[u] = (uint32_t)(key * D + ((slot ^ key) * 8)) * 2u;
+        voff[u] = (uint32_t)(key * D + ((slot ^ (4 * (key & 3)) ^ (2 * ((key >> 2) & 1))) * 8)) * 2u;
+    }
+    // element offsets: page pg, row r of KV head h at pg * pstride + hoff + r * D
+    const uint32_t pstride = (uint32_t)p.Hk * p.P * D, hoff = (uint32_t)h * p.P * D;
+    auto page_base = [&](int raw, int pos) -> uint64_t {
+        return (uint64_t)(uint32_t)clamp_page(raw, p.num_pages) * pstride + hoff + (uint32_t)((pos & (p.P - 1)) * D);
+    };
+    // a tile whose 32 keys are all visible: one page half per wave, scalar row bases
+    auto dl_full = [&](int kt, int buf, const TilePages &tp) {
+        const uint32_t kd = (uint32_t)(uintptr_t)&dsm.k[buf][dx * 2048];
+        const uint32_t vd = (uint32_t)(uintptr_t)&dsm.v[buf][dx * 2048];
+        const uint64_t base = page_base(dx ? tp.pg[1] : tp.pg[0], kt * KT + 16 * dx);
+        const uint16_t *kb = p.kp + base, *vb = p.vp + base;
+#pragma unroll
+        for (int u = 0; u < NQ; u++) {
+            lds_dma16<false>(kb, koff[u], kd + (q0 + u) * 1024);
+            lds_dma16<true>(vb, voff[u], vd + (q0 + u) * 1024);
+        }
+    };
+    // Tile grp is whole for any start when the q-tile's last position alone reaches past it
+    // (the step's keys end at start + t_last + 1 >= t_last + 1): its loads then go out before
+    // the positions load returns.
+    const bool first_full = !INT8 && min(t_first + p.TQ, nb) - 1 - grp * KT >= KT - 1;
+    if (first_full) dl_full(grp, 0, spec);
     u32x4 qreg[NQB];
-    const TilePages spec = tile_pages(p, bt, grp);   // before the positions: tile grp's pages
-    const int start = max(p.positions[tok0], 0), len = start + nb;
     const int qpos = p.causal && row_ok ? start + t : len - 1;
     const int t_last = min(t_first + p.TQ, nb) - 1;
     const int kend = p.causal ? start + t_last + 1 : len;
@@ -824,7 +883,6 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     const int nkt = (kend + KT - 1) / KT;
     const int steps = (nkt + NG - 1) / NG;
     const int mask_from = p.causal ? start + t_first_w : len - 1;
-    Bufs &dsm = reinterpret_cast<Bufs *>(smem_raw)[grp];
 
     f32x4 o[NDB];
 #pragma unroll
@@ -838,38 +896,19 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     const int vrow = 4 * kg + (r16 >> 2), vsw = 4 * (r16 >> 2) ^ 2 * (kg & 1);
     const int vc_lo = (r16 & 3) >> 1, vc_off = 4 * (r16 & 1);
 
-    // direct loads: wave wl issues instructions q0, q0 + 1 of page half dx (instruction q4
-    // writes keys 4 q4 + lane / 16 of the half, 16-B slot lane % 16)
-    const int dx = wl / HW, q0 = NQ * (wl % HW);
-    const int ksub = lane >> 4, slot = lane & 15;
-    uint32_t koff[NQ], voff[NQ];
-#pragma unroll
-    for (int u = 0; u < NQ; u++) {
-        const int key = 4 * (q0 + u) + ksub;
-        koff[u] = (uint32_t)(key * D + ((slot ^ key) * 8)) * 2u;
-        voff[u] = (uint32_t)(key * D + ((slot ^ (4 * (key & 3)) ^ (2 * ((key >> 2) & 1))) * 8)) * 2u;
-    }
     auto dl_load = [&](int kt, int buf, const TilePages &tp) {
         const int pos0 = kt * KT, last = kend - 1 - pos0;   // >= 0 for every tile loaded
         const uint32_t kd = (uint32_t)(uintptr_t)&dsm.k[buf][dx * 2048];
         const uint32_t vd = (uint32_t)(uintptr_t)&dsm.v[buf][dx * 2048];
         if (last >= KT - 1) {
-            const int pg = dx ? tp.pg[1] : tp.pg[0];
-            const long long base = (((long long)pg * p.Hk + h) * p.P + ((pos0 + 16 * dx) & (p.P - 1))) * D;
-            const uint16_t *kb = p.kp + base, *vb = p.vp + base;
-#pragma unroll
-            for (int u = 0; u < NQ; u++) {
-                lds_dma16<false>(kb, koff[u], kd + (q0 + u) * 1024);
-                lds_dma16<true>(vb, voff[u], vd + (q0 + u) * 1024);
-            }
+            dl_full(kt, buf, tp);
         } else {
-            const long long base0 = (((long long)tp.pg[0] * p.Hk + h) * p.P + (pos0 & (p.P - 1))) * D;
-            const long long base1 = (((long long)tp.pg[1] * p.Hk + h) * p.P + ((pos0 + 16) & (p.P - 1))) * D;
+            const uint64_t base0 = page_base(tp.pg[0], pos0), base1 = page_base(tp.pg[1], pos0 + 16);
 #pragma unroll
             for (int u = 0; u < NQ; u++) {
                 const int q4 = q0 + u;
                 const int key = 16 * dx + 4 * q4 + ksub, kk = min(key, last);
-                const long long row = (kk >> 4 ? base1 : base0) + (kk & 15) * D;
+                const uint64_t row = (kk >> 4 ? base1 : base0) + (uint32_t)((kk & 15) * D);
                 const int kc = slot ^ (key & 15), vc = slot ^ (4 * (key & 3)) ^ (2 * ((key >> 2) & 1));
                 lds_dma16_v<false>(p.kp + row + kc * 8, kd + q4 * 1024);
                 lds_dma16_v<true>(p.vp + row + vc * 8, vd + q4 * 1024);
@@ -888,7 +927,7 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     float sts = 0.0f;
     auto i8_row = [&](int kt, int key, const TilePages &tp) -> long long {
         const int pos0 = kt * KT, kk = min(key, kend - 1 - pos0);
-        const int pg = kk >> 4 ? tp.pg[1] : tp.pg[0];
+        const int pg = clamp_page(kk >> 4 ? tp.pg[1] : tp.pg[0], p.num_pages);
         return ((long long)pg * p.Hk + h) * p.P + ((pos0 + (kk & 16)) & (p.P - 1)) + (kk & 15);
     };
     auto i8_load = [&](int kt, const TilePages &tp) {
@@ -943,15 +982,16 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
         float x[8], mt = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            float v = sc[e >> 2][e & 3];
-            if constexpr (INT8) v *= skq[e >> 2][e & 3];
-            if (need_mask) {
-                const int kpos = kt * KT + 16 * (e >> 2) + 4 * kg + (e & 3);
-                v = (kpos <= qpos && kpos < kend_w) ? v : -INFINITY;
-            }
-            x[e] = v;
-            mt = fmaxf(mt, v);
+            x[e] = sc[e >> 2][e & 3];
+            if constexpr (INT8) x[e] *= skq[e >> 2][e & 3];
         }
+        if (need_mask) {   // wave-uniform: only tiles that reach past a row's first visible limit
+            const int lim = min(qpos, kend_w - 1) - (kt * KT + 4 * kg);   // last visible key, tile-relative
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[e] = 16 * (e >> 2) + (e & 3) <= lim ? x[e] : -INFINITY;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) mt = fmaxf(mt, x[e]);
         mt *= p.scale_log2;
         if (__any(mt > m + RESCALE_LOG2)) {
             mt = fmaxf(mt, __shfl_xor(mt, 16));
@@ -995,18 +1035,22 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
 
     auto tile_of = [&](int i) { return grp + NG * i; };
     const int ft = min(tile_of(0), nkt - 1);
-    TilePages pn = ft == grp ? spec : tile_pages(p, bt, ft);
+    TilePages pn = ft == grp ? spec : raw_pages(p, bt, ft);
+    // A step issues the next tile's loads first and looks up the page ids of the tile after
+    // at its end (next_pages), so the scalar loads' wait falls on the step's closing barrier
+    // instead of on its LDS reads (both are counted by lgkmcnt).
     auto issue = [&](int i, int buf) {
-        if (i < steps) {
-            dl_load(min(tile_of(i), nkt - 1), buf, pn);
-            pn = tile_pages(p, bt, min(tile_of(i + 1), nkt - 1));
-        }
+        if (i < steps) dl_load(min(tile_of(i), nkt - 1), buf, pn);
+    };
+    auto next_pages = [&](int i) {
+        if (i < steps) pn = raw_pages(p, bt, min(tile_of(i), nkt - 1));
     };
     if constexpr (!INT8) {
-        issue(0, 0);
+        if (!first_full) issue(0, 0);
+        next_pages(1);
     } else {
         i8_load(min(tile_of(0), nkt - 1), pn);
-        pn = tile_pages(p, bt, min(tile_of(1), nkt - 1));
+        pn = raw_pages(p, bt, min(tile_of(1), nkt - 1));
         i8_store(0);
     }
     wait_direct_loads();   // the queries' direct loads (and tile 0's)
@@ -1037,10 +1081,12 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
                 __syncthreads();
             }
             compute(tile_of(i), 0, [&] { issue(i + 1, 1); });
+            next_pages(i + 2);
             if (i + 1 >= steps) break;
             wait_direct_loads();
             __syncthreads();
             compute(tile_of(i + 1), 1, [&] { issue(i + 2, 0); });
+            next_pages(i + 3);
         }
     } else {
         for (int i = 0; i < steps; i++) {
@@ -1049,7 +1095,7 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
             compute(tile_of(i), i & 1, [&] {
                 if (more) {
                     i8_load(min(tile_of(i + 1), nkt - 1), pn);
-                    pn = tile_pages(p, bt, min(tile_of(i + 2), nkt - 1));
+                    pn = raw_pages(p, bt, min(tile_of(i + 2), nkt - 1));
                 }
             });
             if (more) i8_store((i + 1) & 1);
