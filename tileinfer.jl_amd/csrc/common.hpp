@@ -108,6 +108,13 @@ __device__ __forceinline__ int page_of_s(const int32_t *bt, int idx, int bt_stri
     return p >= num_pages ? num_pages - 1 : p;
 }
 
+// A wave-uniform int32 element as a scalar load (counted by lgkmcnt, never waiting on vector loads).
+__device__ __forceinline__ int sload(const int32_t *a, int idx) {
+    return ((const __attribute__((address_space(4))) int32_t *)a)[__builtin_amdgcn_readfirstlane(idx)];
+}
+// A raw block-table entry as a 0-based page inside the pool (as page_of_s).
+__device__ __forceinline__ int clamp_page(int raw, int num_pages) { return min(max(raw - 1, 0), num_pages - 1); }
+
 }  // namespace ti
 
 // Launchers implemented per kernel file, dispatched by api.hip.

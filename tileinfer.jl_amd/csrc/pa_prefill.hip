@@ -139,10 +139,6 @@ struct Stage {
 
 // Page ids (0-based, clamped into the pool) of the two 16-key halves of tile kt, read with
 // scalar loads; fetched one tile ahead of use so their latency hides behind compute.
-// A wave-uniform int32 element as a scalar load (counted by lgkmcnt, never waiting on vector loads).
-__device__ __forceinline__ int sload(const int32_t *a, int idx) {
-    return ((const __attribute__((address_space(4))) int32_t *)a)[__builtin_amdgcn_readfirstlane(idx)];
-}
 struct TilePages {
     int pg[2];
 };
@@ -159,8 +155,6 @@ __device__ __forceinline__ TilePages raw_pages(const PrefillParams &p, const int
     }
     return tp;
 }
-// A raw block-table entry as a 0-based page inside the pool (as page_of_s).
-__device__ __forceinline__ int clamp_page(int raw, int num_pages) { return min(max(raw - 1, 0), num_pages - 1); }
 
 __device__ __forceinline__ TilePages tile_pages(const PrefillParams &p, const int32_t *bt, int kt) {
     TilePages tp;
@@ -333,8 +327,8 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     const int qtw = PAIR && wl == 1 ? qt_light : qt;
     const int split = PAIR ? 0 : (int)blockIdx.y % p.splits;
     const int b = blockIdx.z;
-    const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
+    const int tok0 = p.qsl ? sload(p.qsl, b) : b * p.nmax;
+    const int nb = p.qsl ? min(sload(p.qsl, b + 1) - tok0, p.nmax) : p.nmax;   // at most max_query_len
     const int t_first = qt * p.TQ;
     if (qt_light * p.TQ >= nb) return;
     const int t_first_w = qtw * p.TQ;
@@ -372,9 +366,9 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
 
     TilePages spec{};
     if constexpr (DL) {
-        if (p.splits == 1) spec = tile_pages(p, bt, grp);
+        if (p.splits == 1) spec = raw_pages(p, bt, grp);
     }
-    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
+    const int start = max(sload(p.positions, tok0), 0), len = start + nb;   // a negative position reads as 0
     const int qpos = p.causal && row_ok ? start + t : len - 1;
     const int t_last = min(t_first + p.TQ, nb) - 1;
     const int kend = p.causal ? start + t_last + 1 : len;
@@ -568,6 +562,12 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
         // Value rows load with cache-policy bits 3 (sc0 sc1), keys with the default policy:
         // measured 12% faster on decode-like verify steps (few queries per sequence, every
         // row read once) and unchanged on long prompts, whose q-tiles re-read the rows.
+        // element offsets: page pg, row r of KV head h at pg * pstride + hoff + r * D (the
+        // page ids arrive raw from the block table and are clamped here)
+        const uint32_t pstride = (uint32_t)p.Hk * p.P * D, hoff = (uint32_t)h * p.P * D;
+        auto page_base = [&](int raw, int pos) -> uint64_t {
+            return (uint64_t)(uint32_t)clamp_page(raw, p.num_pages) * pstride + hoff + (uint32_t)((pos & (p.P - 1)) * D);
+        };
         auto dl_load = [&](int kt, int buf, const TilePages &tp) {
             typedef __attribute__((address_space(3))) void *lds_ptr;
             const int pos0 = kt * KT, last = kend - 1 - pos0;   // >= 0 for every tile loaded
@@ -576,8 +576,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
                 // every key of the tile is a step key: a scalar base and fixed offsets
                 // (selects, not indexing: a dynamically indexed array would be placed in LDS,
                 // whose accesses then wait for every pending direct load)
-                const int pg = dx ? tp.pg[1] : tp.pg[0];
-                const long long base = (((long long)pg * p.Hk + h) * p.P + ((pos0 + 16 * dx) & (p.P - 1))) * D;
+                const uint64_t base = page_base(dx ? tp.pg[1] : tp.pg[0], pos0 + 16 * dx);
                 const char *kb = reinterpret_cast<const char *>(p.kp + base);
                 const char *vb = reinterpret_cast<const char *>(p.vp + base);
 #pragma unroll
@@ -589,38 +588,42 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
             } else {
                 // the step's last tile: keys past its end read the last key's row (finite
                 // data under p = 0); a slot keeps the swizzle of the key it stands for
-                const long long base0 = (((long long)tp.pg[0] * p.Hk + h) * p.P + (pos0 & (p.P - 1))) * D;
-                const long long base1 = (((long long)tp.pg[1] * p.Hk + h) * p.P + ((pos0 + 16) & (p.P - 1))) * D;
+                const uint64_t base0 = page_base(tp.pg[0], pos0), base1 = page_base(tp.pg[1], pos0 + 16);
 #pragma unroll
                 for (int u = 0; u < NQ; u++) {
                     const int q4 = q0 + u;
                     const int key = 16 * dx + 4 * q4 + ksub, kk = min(key, last);
-                    const long long row = (kk >> 4 ? base1 : base0) + (kk & 15) * D;
+                    const uint64_t row = (kk >> 4 ? base1 : base0) + (uint32_t)((kk & 15) * D);
                     const int kc = slot ^ (key & 15), vc = slot ^ (4 * (key & 3));
                     __builtin_amdgcn_global_load_lds(p.kp + row + kc * 8, (lds_ptr)(kd + q4 * 512), 16, 0, 0);
                     __builtin_amdgcn_global_load_lds(p.vp + row + vc * 8, (lds_ptr)(vd + q4 * 512), 16, 0, 3);
                 }
             }
         };
-        // page ids of the next tile to load, fetched one load ahead (the first tile's with
-        // the queries, before the positions, when keys are not split)
+        // raw page ids of the next tile to load, fetched one load ahead (the first tile's
+        // with the queries, before the positions, when keys are not split); a step looks up
+        // the tile after next at its end, so the scalar loads' wait falls on the closing
+        // barrier instead of on the step's LDS reads
         const int ft = min(tile_of(0), kt_hi - 1);
-        TilePages pn = p.splits == 1 && ft == grp ? spec : tile_pages(p, bt, ft);
+        TilePages pn = p.splits == 1 && ft == grp ? spec : raw_pages(p, bt, ft);
         auto issue = [&](int i, int buf) {
-            if (i < steps) {
-                dl_load(min(tile_of(i), kt_hi - 1), buf, pn);
-                pn = tile_pages(p, bt, min(tile_of(i + 1), kt_hi - 1));
-            }
+            if (i < steps) dl_load(min(tile_of(i), kt_hi - 1), buf, pn);
+        };
+        auto next_pages = [&](int i) {
+            if (i < steps) pn = raw_pages(p, bt, min(tile_of(i), kt_hi - 1));
         };
         issue(0, 0);
+        next_pages(1);
         for (int i = 0; i < steps; i += 2) {
             wait_direct_loads();
             __syncthreads();
             compute(tile_of(i), 0, [&] { issue(i + 1, 1); });
+            next_pages(i + 2);
             if (i + 1 >= steps) break;
             wait_direct_loads();
             __syncthreads();
             compute(tile_of(i + 1), 1, [&] { issue(i + 2, 0); });
+            next_pages(i + 3);
         }
         __syncthreads();   // every wave is done with the tiles before the merge reuses the LDS
     } else {

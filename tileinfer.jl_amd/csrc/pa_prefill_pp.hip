@@ -92,11 +92,11 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
     const int qt = p.qtiles - 1 - (int)blockIdx.y / p.splits;   // heaviest q-tiles first
     const int split = (int)blockIdx.y % p.splits;
     const int b = blockIdx.z;
-    const int tok0 = p.qsl ? p.qsl[b] : b * p.nmax;
-    const int nb = p.qsl ? min(p.qsl[b + 1] - tok0, p.nmax) : p.nmax;   // at most max_query_len
+    const int tok0 = p.qsl ? sload(p.qsl, b) : b * p.nmax;
+    const int nb = p.qsl ? min(sload(p.qsl, b + 1) - tok0, p.nmax) : p.nmax;   // at most max_query_len
+    const int start = max(sload(p.positions, tok0), 0), len = start + nb;   // a negative position reads as 0
     const int t_first = qt * p.TQ;
     if (t_first >= nb) return;
-    const int start = max(p.positions[tok0], 0), len = start + nb;   // a negative position reads as 0
     const int t_last = min(t_first + p.TQ, nb) - 1;
     const int kend = p.causal ? start + t_last + 1 : len;
     const int nkt = (kend + KT - 1) / KT;
@@ -123,13 +123,16 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
     const int half = team;                         // == ckey >> 4, wave-uniform
     const long long chunk_off = (long long)(ckey & 15) * D + cch * 8;
 
-    // Page (0-based, clamped into the pool) of this wave's half of tile j (clamped to
-    // the last tile, so loads past the end re-read it and are never stored).
-    auto half_base = [&](int j) -> long long {
-        const int kt = kt_lo + min(j, N - 1);
-        const int pos = kt * KT + 16 * half;
-        const int pg = page_of_s(bt, pos >> p.pshift, p.bt_stride, p.num_pages);
-        return (((long long)pg * p.Hk + h) * p.P + (pos & (p.P - 1))) * D;
+    // This wave's half of tile j (clamped to the last tile, so loads past the end re-read
+    // it and are never stored): its block-table entry (raw_half, a scalar load, looked up a
+    // step before use so its wait does not fall right after it) and its row base in
+    // elements (half_base: page clamped into the pool, 32-bit page stride and head offset).
+    const uint32_t pstride = (uint32_t)p.Hk * p.P * D, hoff = (uint32_t)h * p.P * D;
+    auto half_pos = [&](int j) { return (kt_lo + min(j, N - 1)) * KT + 16 * half; };
+    auto raw_half = [&](int j) { return sload(bt, min(half_pos(j) >> p.pshift, p.bt_stride - 1)); };
+    auto half_base = [&](int raw, int j) -> long long {
+        return (long long)((uint64_t)(uint32_t)clamp_page(raw, p.num_pages) * pstride + hoff +
+                           (uint32_t)((half_pos(j) & (p.P - 1)) * D));
     };
 
     struct Stage {
@@ -168,15 +171,17 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
     // flight in stage 0.
     // (Scheduling fences keep the loads in tile order, so the waits before each LDS
     // store count exactly the younger tiles still in flight.)
-    long long nbase = half_base(0);
+    int r0 = raw_half(0), r1 = raw_half(1), r2 = raw_half(2), r3 = raw_half(3);
+    long long nbase = half_base(r0, 0);
     load(st[0], nbase);
-    nbase = half_base(1);
+    nbase = half_base(r1, 1);
     __builtin_amdgcn_sched_barrier(0);
     load(st[1], nbase);
-    nbase = half_base(2);
+    nbase = half_base(r2, 2);
     __builtin_amdgcn_sched_barrier(0);
     load(st[2], nbase);
-    nbase = half_base(3);
+    nbase = half_base(r3, 3);
+    int nraw = raw_half(4);
     __builtin_amdgcn_sched_barrier(0);
     store_k(st[0], 0);
     store_v(st[0], 0, 0);
@@ -185,7 +190,8 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
     // loop with two different counts of loads in flight, which costs conservative waits.
     store_k(st[1], 1);
     load(st[0], nbase);
-    nbase = half_base(4);
+    nbase = half_base(nraw, 4);
+    nraw = raw_half(5);
 
     f32x16 o[NDB];
 #pragma unroll
@@ -286,7 +292,8 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
         if (i + 2 < N) store_k(st[S2], S2);          // tile i + 2 (loaded at step i - 2)
         if (i + 1 < N) store_v(st[S1], S1, i + 1);   // tile i + 1 (loaded at step i - 3)
         load(st[S1], nbase);                         // tile i + 4
-        nbase = half_base(i + 5);
+        nbase = half_base(nraw, i + 5);
+        nraw = raw_half(i + 6);
         phase_barrier();
     };
     // First tile (relative) whose keys reach past mask_from.
