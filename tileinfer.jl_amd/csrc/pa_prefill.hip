@@ -42,7 +42,7 @@ struct PrefillParams {
     const float *ls, *smooth;
     const int32_t *positions, *qsl, *bt;
     float *part;                       // split partials [B][Hk][splits][M][D + 2]
-    int bt_stride, num_pages, P, pshift, Hk, Hq, G, TQ, nmax, qtiles, causal, splits, M;
+    int bt_stride, num_pages, P, pshift, Hk, Hq, G, gshift, TQ, nmax, qtiles, causal, splits, M;
     float scale_log2;
 };
 
@@ -828,19 +828,23 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     const int nb = p.qsl ? min(sload(p.qsl, b + 1) - tok0, p.nmax) : p.nmax;
     const int start = max(sload(p.positions, tok0), 0), len = start + nb;
     const int t_first = qt * p.TQ;
-    if (qt_light * p.TQ >= nb) return;
+    // No early exit for a pair past the sequence's queries (a shorter sequence of a ragged
+    // batch): a branch here would let the compiler sink the scalar loads above past it, behind
+    // the query rows' address arithmetic. Such a pair has no row to compute (row_ok is false
+    // everywhere, its key steps are at most those of its first positions) and writes nothing.
     const int t_first_w = qtw * p.TQ;
     // This lane's row: row rr of its q-tile (B operand of S^T: elements 32 i + 8 kg .. + 8).
-    const int rr = 16 * (wl & 1) + r16, tl = rr / p.G, t = t_first_w + tl;
+    // (G divides 32 here, a power of two: rows split into position and head by shifts)
+    const int rr = 16 * (wl & 1) + r16, tl = rr >> p.gshift, t = t_first_w + tl;
     const bool row_ok = tl < p.TQ && t < nb && !(light && qt_light == qt);
     // The pair's 64 query rows (heavy 0-31, light 32-63) go to LDS with one direct load per
     // lane (row threadIdx / 16, 16-B slot threadIdx % 16 holding chunk slot ^ (row % 16));
     // each wave reads its operands back once, after the first barrier.
     {
         const int qrow = threadIdx.x >> 4, qslot = threadIdx.x & 15, rl = qrow & 31;
-        const int tq = ((qrow >> 5) ? qt_light : qt) * p.TQ + rl / p.G, gq = rl - (rl / p.G) * p.G;
-        const bool ok = rl / p.G < p.TQ && tq < nb;
-        const uint16_t *src = p.q + ((size_t)(tok0 + (ok ? tq : 0)) * p.Hq + h * p.G + gq) * D + (qslot ^ (qrow & 15)) * 8;
+        const int tq = ((qrow >> 5) ? qt_light : qt) * p.TQ + (rl >> p.gshift), gq = rl & (p.G - 1);
+        const bool ok = (rl >> p.gshift) < p.TQ && tq < nb;
+        const uint16_t *src = p.q + ((size_t)(ok ? tok0 + tq : 0) * p.Hq + h * p.G + gq) * D + (qslot ^ (qrow & 15)) * 8;
         lds_dma16_v<false>(src, (uint32_t)(uintptr_t)(smem_raw + QOFF) + w * 1024);
     }
     Bufs &dsm = reinterpret_cast<Bufs *>(smem_raw)[grp];
@@ -1136,7 +1140,7 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     for (int it = 0; it < IT; it++) {
         const int item = threadIdx.x + it * NT, sr = item / (D / 4), d4 = (item % (D / 4)) * 4;
         const int wr = sr / 32, rl = sr % 32;
-        const int ttl = rl / p.G, gg = rl - ttl * p.G, tt = (wr ? qt_light : qt) * p.TQ + ttl;
+        const int ttl = rl >> p.gshift, gg = rl & (p.G - 1), tt = (wr ? qt_light : qt) * p.TQ + ttl;
         if (wr == 1 && qt_light == qt) continue;
         float mx = NEG_BIG;
 #pragma unroll
@@ -1309,6 +1313,7 @@ int ti_launch_prefill(const ti_attention_args *a, const ti_kv_cache *c, const ti
     p.Hk = c->kv_heads;
     p.Hq = a->q_heads;
     p.G = a->q_heads / c->kv_heads;
+    p.gshift = (p.G & (p.G - 1)) == 0 ? __builtin_ctz(p.G) : -1;   // used by the paired 16-row kernel only
     p.nmax = a->max_query_len;
     p.causal = a->causal;
     p.scale_log2 = a->scale * LOG2E;
