@@ -295,28 +295,27 @@ def main():
     for i in range(args.warmup):
         decode_call(s, i, scale)
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # An event after every WIN calls of the timed region: the spread (min, median) is over
+    # those windows' per-call means, whose average is the mean itself (events around single
+    # calls would add the gap between launches to every call).
+    WIN = 5
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps // WIN + 2)]
     t0 = time.perf_counter()
-    e0.record()
+    marks[0].record()
+    nm = 1
     for i in range(args.steps):
         decode_call(s, i, scale)
-    e1.record()
+        if (i + 1) % WIN == 0 or i + 1 == args.steps:
+            marks[nm].record()
+            nm += 1
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
-    # spread: the same calls again, back to back, with an event every WIN calls; min and
-    # median are over those windows' per-call means (events around single calls would add
-    # the gap between launches to every call)
-    WIN = 5
-    nwin = max(1, args.steps // WIN)
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(nwin + 1)]
-    ev[0].record()
-    for w in range(nwin):
-        for i in range(WIN):
-            decode_call(s, w * WIN + i, scale)
-        ev[w + 1].record()
-    torch.cuda.synchronize()
-    per_call = sorted(ev[w].elapsed_time(ev[w + 1]) * 1e3 / WIN for w in range(nwin))
+    ms = marks[0].elapsed_time(marks[nm - 1]) / args.steps
+    bounds = [min(WIN * w, args.steps) for w in range(nm)]
+    bounds[-1] = args.steps
+    per_call = sorted(marks[w].elapsed_time(marks[w + 1]) * 1e3 / (bounds[w + 1] - bounds[w])
+                      for w in range(nm - 1) if bounds[w + 1] > bounds[w])
+    nwin = len(per_call)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"decode B={B} L={L}: {ms * 1e3:.1f} us/call, {gbs:.0f} GB/s ({wall:.2f} s wall)")
     del s
@@ -450,8 +449,8 @@ def main():
         "us_per_call": round(ms * 1e3, 2),
         "us_per_call_min": round(per_call[0], 2),
         "us_per_call_median": round(per_call[len(per_call) // 2], 2),
-        "us_per_call_spread": f"min and median over {nwin} windows of {WIN} back-to-back calls (per-call mean of each "
-                              "window), timed after the K steps of us_per_call",
+        "us_per_call_spread": f"min and median over the {nwin} windows of up to {WIN} back-to-back calls that make up "
+                              "the timed K steps (per-call mean of each window; us_per_call is their overall mean)",
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
         "higher_is_better": True,
         "scaling": "weak",
