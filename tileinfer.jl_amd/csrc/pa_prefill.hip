@@ -368,7 +368,7 @@ __global__ void __launch_bounds__(64 * WPG * NG) prefill_kernel(PrefillParams p)
     if constexpr (DL) {
         if (p.splits == 1) spec = raw_pages(p, bt, grp);
     }
-    const int start = max(sload(p.positions, tok0), 0), len = start + nb;   // a negative position reads as 0
+    const int start = max(sload(p.positions, nb > 0 ? tok0 : 0), 0), len = start + nb;   // a negative position reads as 0
     const int qpos = p.causal && row_ok ? start + t : len - 1;
     const int t_last = min(t_first + p.TQ, nb) - 1;
     const int kend = p.causal ? start + t_last + 1 : len;
@@ -826,7 +826,7 @@ __global__ void __launch_bounds__(1024) prefill16_kernel(PrefillParams p) {
     const TilePages spec = raw_pages(p, bt, grp);
     const int tok0 = p.qsl ? sload(p.qsl, b) : b * p.nmax;
     const int nb = p.qsl ? min(sload(p.qsl, b + 1) - tok0, p.nmax) : p.nmax;
-    const int start = max(sload(p.positions, tok0), 0), len = start + nb;
+    const int start = max(sload(p.positions, nb > 0 ? tok0 : 0), 0), len = start + nb;
     const int t_first = qt * p.TQ;
     // No early exit for a pair past the sequence's queries (a shorter sequence of a ragged
     // batch): a branch here would let the compiler sink the scalar loads above past it, behind

@@ -94,7 +94,7 @@ __global__ void __launch_bounds__(64 * NW) prefill_pp_kernel(PPParams p) {
     const int b = blockIdx.z;
     const int tok0 = p.qsl ? sload(p.qsl, b) : b * p.nmax;
     const int nb = p.qsl ? min(sload(p.qsl, b + 1) - tok0, p.nmax) : p.nmax;   // at most max_query_len
-    const int start = max(sload(p.positions, tok0), 0), len = start + nb;   // a negative position reads as 0
+    const int start = max(sload(p.positions, nb > 0 ? tok0 : 0), 0), len = start + nb;   // a negative position reads as 0
     const int t_first = qt * p.TQ;
     if (t_first >= nb) return;
     const int t_last = min(t_first + p.TQ, nb) - 1;
